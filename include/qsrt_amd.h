@@ -1,0 +1,63 @@
+/*
+ * qsrt_amd.h -- C ABI of the MI355X (gfx950) QSRT encoder hot path.
+ *
+ * All pointers are device pointers unless stated otherwise; every call is
+ * asynchronous on `stream` (a hipStream_t passed as void*), allocates
+ * nothing, and returns 0 on success or a negative status:
+ *   -1 bad argument, -2 workspace too small, -3 HIP runtime error.
+ * qsrt_last_error() returns a thread-local message for the last failure.
+ * The caller owns all memory.  No process-global mutable state: the LUT is
+ * passed per call (unlike the reference's __constant__ table pointer,
+ * qsrt/csrc/sqg_quantize.cu:14, :698-705).
+ */
+#ifndef QSRT_AMD_H
+#define QSRT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ABI revision of this header. */
+int qsrt_abi_version(void);
+
+/* Message for the last failing call on this thread. */
+const char *qsrt_last_error(void);
+
+/*
+ * Bytes of traceback workspace qsrt_viterbi_tiles needs for `n_tiles` tiles
+ * at rate K on the current device (one 256-row decision buffer per
+ * workgroup, at most one workgroup per compute unit).  0 on error.
+ * Replaces the workspace sizing of qsrt/sqg_quantizer.py:410-427
+ * (_sqg_temp_buffers).
+ */
+size_t qsrt_viterbi_workspace_bytes(int K, int64_t n_tiles);
+
+/*
+ * Tail-biting L16 trellis quantization of `n_tiles` 256-weight tiles.
+ *   tiles   f32 [n_tiles, 256]  targets in tensor-core order
+ *   recon   f32 [n_tiles, 256]  out: E4M3 label of each emitted codeword
+ *   states  u16 [n_tiles, 256]  out: 16-bit codewords (closed cyclic path)
+ *   K       2, 3 or 4 branch bits per weight
+ *   tailbite_context  1..128 primer half-width C
+ *   lut_e4m3  u8 [65536] state(codeword)-indexed E4M3 labels
+ *   boundary_lag  0: boundary = argmin of the primer's final costs
+ *                 1: argmin of the costs one step earlier
+ *   workspace  >= qsrt_viterbi_workspace_bytes(K, n_tiles) bytes
+ * FP32 path metrics, lowest-index ties (see oracle/viterbi_ref.c).
+ * Replaces quantize_tiles_sqg_cuda (qsrt/csrc/sqg_quantize.cu:651-783) and
+ * the kernels it launches (qsrt_quantize_tiles_kernel.cuh:26-500,
+ * qsrt_quantize_tiles_k2_kernel.cuh:47-366); bound from Python where the
+ * reference binds `quantize_tiles_sqg` (qsrt/csrc/sqg_quantize.cpp:56-59).
+ */
+int qsrt_viterbi_tiles(const float *tiles, float *recon, uint16_t *states, int64_t n_tiles, int K,
+                       int tailbite_context, const uint8_t *lut_e4m3, int boundary_lag, void *workspace,
+                       size_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QSRT_AMD_H */

@@ -1,0 +1,166 @@
+/*
+ * Oracle: tail-biting tile Viterbi in plain FP32 C -- TEST INFRASTRUCTURE ONLY.
+ *
+ * CPU restatement of the reference's tile quantizer pass structure
+ * (qsrt/csrc/qsrt_quantize_tiles_kernel.cuh:79-499 and
+ * qsrt/csrc/qsrt_quantize_tiles_k2_kernel.cuh:233-365), parametric in the
+ * codeword width L (16 in production), the branch bits K, the tile length
+ * T (256) and the tail-bite context C, so that tiny trellises can be
+ * checked by exhaustive search.
+ *
+ * Arithmetic contract (this is what the HIP kernel must reproduce bit for
+ * bit; the reference kernels use FP16 and differ by design):
+ *   d = label - x                        (FP32 subtract)
+ *   c = fmaf(d, d, predecessor_cost)     (one rounding; step 0 adds +0)
+ *   per-state choice: lowest predecessor index k among equal minima
+ *   boundary choice:  lowest state index among equal minima
+ *   unreachable edges carry +inf (constrained first step only).
+ * Built with -ffp-contract=off and without fast-math.
+ *
+ * Trellis: codeword w has L bits; state = w & (2^(L-K) - 1); the codeword
+ * entering state s from predecessor choice k is (k << (L-K)) | s and that
+ * predecessor state is (k << (L-2K)) | (s >> K).
+ *
+ * Passes per tile (reference qsrt_quantize_tiles_kernel.cuh:494-499):
+ *   1. primer: positions T-C .. T-1, 0 .. C-1 from a free start, decisions
+ *      kept for positions 0 .. C-1;
+ *   2. boundary = argmin of the primer's final costs (boundary_lag = 0, the
+ *      K2 kernel, qsrt_quantize_tiles_k2_kernel.cuh:274-325) or of the
+ *      costs one step earlier (boundary_lag = 1, what the generic kernel
+ *      reads after its last buffer swap, qsrt_quantize_tiles_kernel.cuh:360-441);
+ *   3. trace back to the state before position 0 (end_state);
+ *   4. constrained pass over positions 0 .. T-1 whose first step only admits
+ *      predecessor end_state;
+ *   5. trace back from end_state at position T-1, emitting codewords and
+ *      labels (qsrt_quantize_tiles_kernel.cuh:443-487).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+typedef struct {
+    int L, K, T, S, P;
+    float *a, *b;      /* cost ping-pong, S floats each */
+    uint8_t *dec;      /* T * S decisions */
+} vt_ctx;
+
+/* One forward pass; returns the buffer holding the final costs and, via
+ * *penult, the buffer holding the costs one step earlier. */
+static float *vt_forward(vt_ctx *c, const float *lab, const float *x, int roll, int steps,
+                         int pre_state, int trace_start, float **penult)
+{
+    const int S = c->S, P = c->P, K = c->K, L = c->L;
+    const int pred_shift = L - 2 * K, word_shift = L - K;
+    float *prev = c->a, *next = c->b;
+    for (int i = 0; i < steps; ++i) {
+        const int pos = (i + roll) % c->T;
+        const float w = x[pos];
+        const int record = i >= trace_start;
+        uint8_t *drow = c->dec + (size_t)pos * S;
+        for (int s = 0; s < S; ++s) {
+            const int q = s >> K;
+            float best = 0.0f;
+            int arg = 0;
+            for (int k = 0; k < P; ++k) {
+                const float d = lab[(k << word_shift) | s] - w;
+                float cost;
+                if (i == 0) {
+                    const int pred = (k << pred_shift) | q;
+                    cost = (pre_state < 0 || pred == pre_state) ? fmaf(d, d, 0.0f) : INFINITY;
+                } else {
+                    cost = fmaf(d, d, prev[(k << pred_shift) | q]);
+                }
+                if (k == 0 || cost < best) {
+                    best = cost;
+                    arg = k;
+                }
+            }
+            next[s] = best;
+            if (record) drow[s] = (uint8_t)arg;
+        }
+        float *t = prev;
+        prev = next;
+        next = t;
+    }
+    *penult = next;
+    return prev;
+}
+
+static int vt_argmin(const float *cost, int S)
+{
+    int arg = 0;
+    for (int s = 1; s < S; ++s)
+        if (cost[s] < cost[arg]) arg = s;
+    return arg;
+}
+
+static int vt_trace(const vt_ctx *c, int roll, int steps, int edge, const float *lab,
+                    uint16_t *states, float *recon)
+{
+    const int K = c->K, pred_shift = c->L - 2 * c->K;
+    for (int i = steps - 1; i >= 0; --i) {
+        const int pos = (i + roll) % c->T;
+        const int k = c->dec[(size_t)pos * c->S + edge];
+        const int prev = (k << pred_shift) | (edge >> K);
+        if (states) {
+            const int word = (prev << K) | edge;
+            states[pos] = (uint16_t)word;
+            recon[pos] = lab[word];
+        } else if (pos == 0) {
+            return prev;
+        }
+        edge = prev;
+    }
+    return edge;
+}
+
+/*
+ * tiles, recon: [n_tiles, T] float; states: [n_tiles, T] uint16;
+ * labels: [2^L] float, state(codeword)-indexed; boundary (optional):
+ * [n_tiles] int32 receiving end_state.  Returns 0, or -1 on bad arguments,
+ * -2 on allocation failure.
+ */
+int qsrt_oracle_viterbi(const float *tiles, float *recon, uint16_t *states, int64_t n_tiles,
+                        int L, int K, int T, int C, const float *labels, int boundary_lag,
+                        int32_t *boundary, int n_threads)
+{
+    if (L < 2 || L > 16 || K < 1 || 2 * K > L || T < 2 || C < 1 || 2 * C > T ||
+        (boundary_lag != 0 && boundary_lag != 1) || n_tiles < 0)
+        return -1;
+    int failed = 0;
+#ifdef _OPENMP
+    if (n_threads > 0) omp_set_num_threads(n_threads);
+#else
+    (void)n_threads;
+#endif
+#pragma omp parallel reduction(| : failed)
+    {
+        vt_ctx c;
+        c.L = L; c.K = K; c.T = T; c.S = 1 << (L - K); c.P = 1 << K;
+        c.a = (float *)malloc(sizeof(float) * c.S);
+        c.b = (float *)malloc(sizeof(float) * c.S);
+        c.dec = (uint8_t *)calloc((size_t)T * c.S, 1);
+        if (!c.a || !c.b || !c.dec) failed = 1;
+#pragma omp for schedule(dynamic, 1)
+        for (int64_t t = 0; t < n_tiles; ++t) {
+            if (failed) continue;
+            const float *x = tiles + t * T;
+            float *penult;
+            float *fin = vt_forward(&c, labels, x, T - C, 2 * C, -1, C, &penult);
+            const int start = vt_argmin(boundary_lag ? penult : fin, c.S);
+            const int end_state = vt_trace(&c, T - C, 2 * C, start, labels, NULL, NULL);
+            vt_forward(&c, labels, x, 0, T, end_state, 0, &penult);
+            vt_trace(&c, 0, T, end_state, labels, states + t * T, recon + t * T);
+            if (boundary) boundary[t] = end_state;
+        }
+        free(c.a);
+        free(c.b);
+        free(c.dec);
+    }
+    return failed ? -2 : 0;
+}
