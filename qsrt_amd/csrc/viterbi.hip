@@ -18,7 +18,11 @@
 //   * decisions are packed (2 bits at K2, a nibble at K3/K4) into one
 //     coalesced store per thread per step, in a per-workgroup HBM buffer;
 //   * the boundary argmin is a wave64 shuffle reduction with lowest-index
-//     ties; tracebacks run on one lane with agent-scope loads.
+//     ties;
+//   * passes are pipelined over two tiles per workgroup (P0, P1, F0, P2,
+//     F1, ...): each traceback runs on one lane, one position per step of
+//     the next pass, its dependent decision loads hidden behind the step;
+//     a traceback with nothing to hide behind runs speculatively on wave 0.
 //
 // Arithmetic contract (bit-exact with oracle/viterbi_ref.c): see that file.
 
@@ -39,32 +43,25 @@ struct Geo;
 template <>
 struct Geo<2> {
     static constexpr int S = 1 << 14, P = 4, NG = 4, NS = 4, kPredStride = 1 << 12;
-    static constexpr int kRowBytes = kThreads * 4, kDecBits = 2;
+    static constexpr int kRowBytes = kThreads * 4;
     __device__ static int group(int t, int j) { return t + kThreads * j; }
     __device__ static int first_state(int t, int j) { return 4 * group(t, j); }
     // field f = 4 j + e sits at bits [2 (15 - f), +2)
-    __device__ static int decision(const uint8_t* row, int s) {
-        const int q = s >> 2;
-        const uint32_t w = __hip_atomic_load(reinterpret_cast<const uint32_t*>(row) + (q & (kThreads - 1)),
-                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return (w >> (2 * (15 - (4 * (q >> 10) + (s & 3))))) & 3;
-    }
+    __device__ static int word_index(int s) { return (s >> 2) & (kThreads - 1); }
+    __device__ static int extract(uint32_t w, int s) { return (w >> (2 * (15 - (4 * (s >> 12) + (s & 3))))) & 3; }
 };
 
 // K3: 8192 states, groups of 8 states with predecessors q + 1024 k.
-// Thread t owns group q = t; decisions are nibbles.
+// Thread t owns group q = t; 3-bit decisions, 24 bits used per dword.
 template <>
 struct Geo<3> {
     static constexpr int S = 1 << 13, P = 8, NG = 1, NS = 8, kPredStride = 1 << 10;
-    static constexpr int kRowBytes = kThreads * 4, kDecBits = 4;
+    static constexpr int kRowBytes = kThreads * 4;
     __device__ static int group(int t, int) { return t; }
     __device__ static int first_state(int t, int) { return 8 * t; }
-    // state 8 t + e sits at bits [4 (7 - e), +4)
-    __device__ static int decision(const uint8_t* row, int s) {
-        const uint32_t w = __hip_atomic_load(reinterpret_cast<const uint32_t*>(row) + (s >> 3),
-                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return (w >> (4 * (7 - (s & 7)))) & 7;
-    }
+    // state 8 t + e sits at bits [3 (7 - e), +3)
+    __device__ static int word_index(int s) { return s >> 3; }
+    __device__ static int extract(uint32_t w, int s) { return (w >> (3 * (7 - (s & 7)))) & 7; }
 };
 
 // K4: 4096 states, groups of 16 states with predecessors q + 256 k.
@@ -72,17 +69,22 @@ struct Geo<3> {
 template <>
 struct Geo<4> {
     static constexpr int S = 1 << 12, P = 16, NG = 1, NS = 4, kPredStride = 1 << 8;
-    static constexpr int kRowBytes = kThreads * 2, kDecBits = 4;
+    static constexpr int kRowBytes = kThreads * 2;
     __device__ static int group(int t, int) { return t >> 2; }
     __device__ static int first_state(int t, int) { return 4 * t; }
     // thread t's 16-bit field holds state 4 t + e at bits [4 (3 - e), +4);
     // little-endian: even threads in the low half of each dword.
-    __device__ static int decision(const uint8_t* row, int s) {
-        const uint32_t w = __hip_atomic_load(reinterpret_cast<const uint32_t*>(row) + (s >> 3),
-                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return (w >> (16 * ((s >> 2) & 1) + 4 * (3 - (s & 3)))) & 15;
-    }
+    __device__ static int word_index(int s) { return s >> 3; }
+    __device__ static int extract(uint32_t w, int s) { return (w >> (16 * ((s >> 2) & 1) + 4 * (3 - (s & 3)))) & 15; }
 };
+
+// Decision word holding state s at tile position `pos` (workgroup-scope:
+// the writers are this workgroup's other waves, fenced before a barrier).
+template <int K>
+__device__ __forceinline__ uint32_t load_decisions(const uint8_t* dec, int pos, int s) {
+    const uint32_t* row = reinterpret_cast<const uint32_t*>(dec + static_cast<size_t>(pos) * Geo<K>::kRowBytes);
+    return __hip_atomic_load(row + Geo<K>::word_index(s), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
 
 template <int K>
 struct Labels {
@@ -91,20 +93,67 @@ struct Labels {
 
 __device__ __forceinline__ float fmin2(float a, float b) { return __builtin_fminf(a, b); }
 
-// One trellis step over all states.  FIRST: no predecessor costs (the
-// reference's step 0); CONSTRAINED: only predecessor `pre_state` is
-// admissible at step 0; RECORD: pack and store decisions for this row.
-template <int K, bool FIRST, bool CONSTRAINED, bool RECORD>
+// word = 2 * word + (lane's bit of `mask`): one v_addc_co_u32 with the lane
+// mask as carry-in, instead of select-then-shift-or.
+__device__ __forceinline__ uint32_t push_bit(uint32_t word, uint64_t mask) {
+    uint32_t out;
+    uint64_t carry_out;
+    asm("v_addc_co_u32_e64 %0, %1, %2, %2, %3" : "=v"(out), "=s"(carry_out) : "v"(word), "s"(mask));
+    return out;
+}
+
+// word = (word << B) | value in one v_lshl_or_b32.  Opaque to the compiler
+// on purpose: a visible constant shift gets folded into the index selects,
+// which then materialise dozens of pre-shifted constants in VGPRs.
+template <int B>
+__device__ __forceinline__ uint32_t push_bits(uint32_t word, uint32_t value) {
+    uint32_t out;
+    asm("v_lshl_or_b32 %0, %1, %2, %3" : "=v"(out) : "v"(word), "i"(B), "v"(value));
+    return out;
+}
+
+// Pack the lowest-index argmin of c[0..P) (value m) into `word`, K bits, MSB
+// first.  The P-1 equality tests are wave ballots (SGPR lane masks); the
+// prefix masks ge[k] = "argmin >= k" and the bit masks are scalar-unit
+// algebra, leaving K VALU ops for the insertion.
+template <int K>
+__device__ __forceinline__ uint32_t push_argmin(uint32_t word, const float (&c)[1 << K], float m) {
+    constexpr int P = 1 << K;
+    uint64_t ge[P + 1];
+    ge[0] = ~0ull;
+#pragma unroll
+    for (int k = 0; k < P - 1; ++k) ge[k + 1] = ge[k] & ~__builtin_amdgcn_ballot_w64(c[k] == m);
+    ge[P] = 0;
+#pragma unroll
+    for (int b = K - 1; b >= 0; --b) {
+        uint64_t bit = 0;
+#pragma unroll
+        for (int lo = 1 << b; lo < P; lo += 2 << b) bit |= ge[lo] & ~ge[lo + (1 << b)];
+        word = push_bit(word, bit);
+    }
+    return word;
+}
+
+// One trellis step over all states.  On the first step of a pass (FIRST)
+// there are no predecessor costs: every predecessor starts at 0, or, in the
+// constrained pass, only `pre_state` starts at 0 and the others at +inf
+// (fma(d, d, 0) == d * d and fma(d, d, inf) == inf, so this is exactly the
+// reference's step-0 rule).  RECORD: pack and store this row's decisions.
+template <int K, bool RECORD, bool FIRST>
 __device__ __forceinline__ void trellis_step(const Labels<K>& lab, const float* __restrict__ prev,
                                              float* __restrict__ next, float x, int pre_state,
-                                             uint8_t* __restrict__ dec_row, int t, uint32_t dec_bits) {
+                                             uint8_t* __restrict__ dec_row, int t) {
     using G = Geo<K>;
     uint32_t word = 0;
 #pragma unroll
     for (int j = 0; j < G::NG; ++j) {
         const int q = G::group(t, j);
         float p[G::P];
-        if constexpr (!FIRST) {
+        if constexpr (FIRST) {
+#pragma unroll
+            for (int k = 0; k < G::P; ++k)
+                p[k] = (pre_state < 0 || q + k * G::kPredStride == pre_state) ? 0.0f : __builtin_inff();
+        } else {
 #pragma unroll
             for (int k = 0; k < G::P; ++k) p[k] = prev[q + k * G::kPredStride];
         }
@@ -115,25 +164,27 @@ __device__ __forceinline__ void trellis_step(const Labels<K>& lab, const float* 
 #pragma unroll
             for (int k = 0; k < G::P; ++k) {
                 const float d = lab.v[j][e][k] - x;
-                if constexpr (FIRST) {
-                    c[k] = __builtin_fmaf(d, d, 0.0f);
-                    if constexpr (CONSTRAINED) {
-                        if (q + k * G::kPredStride != pre_state) c[k] = __builtin_inff();
-                    }
-                } else {
-                    c[k] = __builtin_fmaf(d, d, p[k]);
-                }
+                c[k] = __builtin_fmaf(d, d, p[k]);
             }
             float m = c[0];
 #pragma unroll
             for (int k = 1; k < G::P; ++k) m = fmin2(m, c[k]);
             best[e] = m;
             if constexpr (RECORD) {
-                int arg = G::P - 1;
+                if constexpr (K <= 3) {
+                    word = push_argmin<K>(word, c, m);
+                } else {
+                    // 16 predecessors: the mask algebra would cost ~37 scalar
+                    // ops per state, so select the index in VGPRs instead.
+                    int arg = G::P - 1;
 #pragma unroll
-                for (int k = G::P - 2; k >= 0; --k) arg = (c[k] == m) ? k : arg;
-                word = (word << dec_bits) | static_cast<uint32_t>(arg);
+                    for (int k = G::P - 2; k >= 0; --k) arg = (c[k] == m) ? k : arg;
+                    word = push_bits<K>(word, static_cast<uint32_t>(arg));
+                }
             }
+            // One state at a time: four waves per SIMD already hide latency,
+            // and overlapping states would push the labels out of VGPRs.
+            __builtin_amdgcn_sched_barrier(0);
         }
         float* dst = next + G::first_state(t, j);
 #pragma unroll
@@ -179,55 +230,133 @@ __device__ int boundary_argmin(const float* cost, float* red_v, int* red_i, int 
     return bi;
 }
 
-// Single-lane traceback over `steps` rows ending at `edge` (the state after
-// the last step).  With `out_states` null it stops after position 0 and
-// returns the state before it; otherwise it emits codewords and labels.
+// Traceback on wave 0 alone, for tracebacks with no pass to hide behind.
+// Positions top, top-1, ..., 0 are resolved from `edge` (the state after
+// position `top`), D = floor(6 / K) per memory round trip: lane l guesses
+// the next D branch choices (its base-2^K digits), loads the D decisions of
+// its candidate states independently, and the one lane whose guesses all
+// match the stored decisions supplies the state D steps back (ballot +
+// shuffle, no barrier).  Codewords go to `words` when it is non-null.
+// Returns the state before position 0 (uniform across wave 0).
 template <int K>
-__device__ int traceback(const uint8_t* dec, int roll, int steps, int edge, uint16_t* out_states,
-                         float* out_recon, const uint8_t* __restrict__ lut) {
-    using G = Geo<K>;
-    for (int i = steps - 1; i >= 0; --i) {
-        const int pos = (i + roll) & (kTile - 1);
-        const int k = G::decision(dec + static_cast<size_t>(pos) * G::kRowBytes, edge);
-        const int prev = (k << (16 - 2 * K)) | (edge >> K);
-        if (out_states) {
-            const int word = (prev << K) | edge;
-            out_states[pos] = static_cast<uint16_t>(word);
-            out_recon[pos] = qsrt::e4m3_to_float(lut[word]);
-        } else if (pos == 0) {
-            return prev;
+__device__ int traceback_wave(const uint8_t* dec, int top, int edge, uint16_t* words, int lane) {
+    constexpr int P = 1 << K;
+    constexpr int D = 6 / K;
+    int pos = top;
+    while (pos >= 0) {
+        const int d = pos + 1 < D ? pos + 1 : D;
+        int state[D + 1];
+        state[0] = edge;
+        bool ok = lane < (1 << (K * d));
+#pragma unroll
+        for (int j = 1; j <= D; ++j) {
+            if (j <= d) {
+                const int k = (lane >> (K * (j - 1))) & (P - 1);
+                const uint32_t w = load_decisions<K>(dec, pos - j + 1, state[j - 1]);
+                ok = ok & (Geo<K>::extract(w, state[j - 1]) == k);
+                state[j] = (k << (16 - 2 * K)) | (state[j - 1] >> K);
+            }
         }
-        edge = prev;
+        const uint64_t hit = __builtin_amdgcn_ballot_w64(ok);
+        const int src = __builtin_ctzll(hit);
+        int back = state[1];
+#pragma unroll
+        for (int j = 2; j <= D; ++j)
+            if (j == d) back = state[j];
+        if (words && lane == src) {
+#pragma unroll
+            for (int j = 1; j <= D; ++j)
+                if (j <= d) words[pos - j + 1] = static_cast<uint16_t>((state[j] << K) | state[j - 1]);
+        }
+        edge = __shfl(back, src, 64);
+        pos -= d;
     }
     return edge;
 }
 
+// One traceback position, executed by lane 0 inside another pass's step
+// loop: consume the decision word loaded one step earlier (its latency is
+// hidden behind the step), record the codeword, load the next word.
+template <int K>
+__device__ __forceinline__ void trace_advance(const uint8_t* dec, uint16_t* words, int& pos, int& edge,
+                                              uint32_t& pending) {
+    const int k = Geo<K>::extract(pending, edge);
+    const int prev = (k << (16 - 2 * K)) | (edge >> K);
+    if (words) words[pos] = static_cast<uint16_t>((prev << K) | edge);
+    edge = prev;
+    --pos;
+    if (pos >= 0) pending = load_decisions<K>(dec, pos, edge);
+}
+
+// A traceback being overlapped with the next forward pass.  `kind` and the
+// pointers are uniform; pos / edge / pending are meaningful in lane 0 only.
+struct TraceJob {
+    int kind = 0;  // 0 none, 1 primer (yields end_state), 2 final (yields codewords)
+    int tile = -1;
+    const uint8_t* dec = nullptr;
+    uint16_t* words = nullptr;
+    int pos = -1, edge = 0;
+    uint32_t pending = 0;
+};
+
+// One forward pass of `steps` steps over positions roll, roll+1, ... (mod
+// 256), recording decisions from step `trace_start` on, with the pending
+// traceback `job` advanced one position per step by lane 0.
 template <int K>
 __device__ __forceinline__ void forward_pass(const Labels<K>& lab, const float* sx, float*& prev, float*& next, int roll,
-                             int steps, int pre_state, int trace_start, uint8_t* dec, int t,
-                                             uint32_t dec_bits) {
-    using G = Geo<K>;
+                                             int steps, int pre_state, int trace_start, uint8_t* dec, int t,
+                                             TraceJob& job) {
     {
         const int pos = roll & (kTile - 1);
-        uint8_t* row = dec + static_cast<size_t>(pos) * G::kRowBytes;
-        if (pre_state >= 0)
-            trellis_step<K, true, true, true>(lab, prev, next, sx[pos], pre_state, row, t, dec_bits);
-        else if (trace_start == 0)
-            trellis_step<K, true, false, true>(lab, prev, next, sx[pos], -1, row, t, dec_bits);
+        uint8_t* row = dec + static_cast<size_t>(pos) * Geo<K>::kRowBytes;
+        if (trace_start == 0)
+            trellis_step<K, true, true>(lab, prev, next, sx[pos], pre_state, row, t);
         else
-            trellis_step<K, true, false, false>(lab, prev, next, sx[pos], -1, row, t, dec_bits);
+            trellis_step<K, false, true>(lab, prev, next, sx[pos], pre_state, row, t);
+        if (job.kind && t == 0 && job.pos >= 0) trace_advance<K>(job.dec, job.words, job.pos, job.edge, job.pending);
         __syncthreads();
         float* tmp = prev; prev = next; next = tmp;
     }
     for (int i = 1; i < steps; ++i) {
         const int pos = (i + roll) & (kTile - 1);
-        uint8_t* row = dec + static_cast<size_t>(pos) * G::kRowBytes;
+        uint8_t* row = dec + static_cast<size_t>(pos) * Geo<K>::kRowBytes;
         if (i >= trace_start)
-            trellis_step<K, false, false, true>(lab, prev, next, sx[pos], -1, row, t, dec_bits);
+            trellis_step<K, true, false>(lab, prev, next, sx[pos], -1, row, t);
         else
-            trellis_step<K, false, false, false>(lab, prev, next, sx[pos], -1, row, t, dec_bits);
+            trellis_step<K, false, false>(lab, prev, next, sx[pos], -1, row, t);
+        if (job.kind && t == 0 && job.pos >= 0) trace_advance<K>(job.dec, job.words, job.pos, job.edge, job.pending);
         __syncthreads();
         float* tmp = prev; prev = next; next = tmp;
+    }
+}
+
+// Resolve whatever is left of `job` on wave 0 (lane 0 hands over its
+// position).  Every thread must call it; returns after a barrier.  For a
+// primer job the state before position 0 is stored to *end_state.
+template <int K>
+__device__ void finish_job(TraceJob& job, int* end_state, int t) {
+    if (t < 64) {
+        const int pos = __shfl(job.pos, 0, 64);
+        const int edge = __shfl(job.edge, 0, 64);
+        const int result = traceback_wave<K>(job.dec, pos, edge, job.words, t);
+        if (t == 0 && job.kind == 1) *end_state = result;
+    }
+    __syncthreads();
+}
+
+// Start a traceback of the pass that just ended; the caller has fenced the
+// pass's decision stores and passed a barrier.
+template <int K>
+__device__ __forceinline__ void start_job(TraceJob& job, int kind, int tile, const uint8_t* dec, uint16_t* words,
+                                          int top, int edge, int t) {
+    job.kind = kind;
+    job.tile = tile;
+    job.dec = dec;
+    job.words = words;
+    if (t == 0) {
+        job.pos = top;
+        job.edge = edge;
+        job.pending = load_decisions<K>(dec, top, edge);
     }
 }
 
@@ -235,20 +364,20 @@ template <int K>
 __global__ __launch_bounds__(kThreads, 1) void viterbi_tiles_kernel(
     const float* __restrict__ tiles, float* __restrict__ recon, uint16_t* __restrict__ states,
     int64_t n_tiles, int context, const uint8_t* __restrict__ lut, int boundary_lag,
-    uint8_t* __restrict__ dec_ws, uint32_t dec_bits) {
-    // dec_bits == Geo<K>::kDecBits, passed at run time on purpose: with a
-    // compile-time shift the compiler folds the shifts into the argmin
-    // selects and materialises ~30 pre-shifted constants in VGPRs.
+    uint8_t* __restrict__ dec_ws) {
     using G = Geo<K>;
     __shared__ __align__(16) float cost_a[G::S];
     __shared__ __align__(16) float cost_b[G::S];
-    __shared__ float sx[kTile];
+    __shared__ float sx[2][kTile];
+    __shared__ uint16_t words[2][kTile];
+    __shared__ int end_state[2];
     __shared__ float red_v[kWaves];
     __shared__ int red_i[kWaves];
     __shared__ int bcast;
 
     const int t = threadIdx.x;
-    uint8_t* dec = dec_ws + static_cast<size_t>(blockIdx.x) * kTile * G::kRowBytes;
+    constexpr size_t kBufBytes = static_cast<size_t>(kTile) * G::kRowBytes;
+    uint8_t* dec_base = dec_ws + static_cast<size_t>(blockIdx.x) * 2 * kBufBytes;
 
     Labels<K> lab;
 #pragma unroll
@@ -259,29 +388,74 @@ __global__ __launch_bounds__(kThreads, 1) void viterbi_tiles_kernel(
             for (int k = 0; k < G::P; ++k)
                 lab.v[j][e][k] = qsrt::e4m3_to_float(lut[(k << (16 - K)) | (G::first_state(t, j) + e)]);
 
-    for (int64_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
-        if (t < kTile) sx[t] = tiles[tile * kTile + t];
+    // This workgroup's tiles are first + i * stride, i < m.  Passes run in
+    // the order P0, P1, F0, P2, F1, ..., F(m-1) (primer of tile i+1 before
+    // the constrained pass of tile i) so that every traceback can hide
+    // behind the pass after the one that produced it.  Pass n writes
+    // decision buffer n & 1; tile i lives in LDS slot i & 1.
+    const int64_t first = blockIdx.x, stride = gridDim.x;
+    const int m = first < n_tiles ? static_cast<int>((n_tiles - first + stride - 1) / stride) : 0;
+
+    auto finalize = [&](int i) {  // codewords of tile i are complete in words[i & 1]
+        if (t < kTile) {
+            const int64_t tile = first + static_cast<int64_t>(i) * stride;
+            const uint32_t w = words[i & 1][t];
+            states[tile * kTile + t] = static_cast<uint16_t>(w);
+            recon[tile * kTile + t] = qsrt::e4m3_to_float(lut[w]);
+        }
+    };
+
+    TraceJob job;
+    int next_p = 0, next_f = 0;
+    for (int n = 0; next_f < m; ++n) {
+        const bool primer = next_p < m && next_p <= next_f + 1;
+        const int i = primer ? next_p : next_f;
+        const int slot = i & 1;
+        uint8_t* dec = dec_base + static_cast<size_t>(n & 1) * kBufBytes;
+        if (primer) {
+            if (t < kTile) sx[slot][t] = tiles[(first + static_cast<int64_t>(i) * stride) * kTile + t];
+        } else if (job.kind == 1 && job.tile == i) {
+            // Nothing ran between this tile's primer and its constrained
+            // pass: resolve the boundary now.
+            finish_job<K>(job, &end_state[slot], t);
+            job.kind = 0;
+        }
         __syncthreads();
 
+        // Primer: positions 256-C .. 255, 0 .. C-1, decisions kept for 0 .. C-1.
+        // Constrained pass: positions 0 .. 255 from the boundary state.
         float* prev = cost_a;
         float* next = cost_b;
-        // Primer over positions 256-C .. 255, 0 .. C-1; decisions kept for 0 .. C-1.
-        forward_pass<K>(lab, sx, prev, next, kTile - context, 2 * context, -1, context, dec, t, dec_bits);
-        __threadfence();
-        const int start = boundary_argmin<K>(boundary_lag ? next : prev, red_v, red_i, t);
-        if (t == 0) bcast = traceback<K>(dec, kTile - context, 2 * context, start, nullptr, nullptr, lut);
-        __syncthreads();
-        const int end_state = bcast;
+        forward_pass<K>(lab, sx[slot], prev, next, primer ? kTile - context : 0, primer ? 2 * context : kTile,
+                        primer ? -1 : end_state[slot], primer ? context : 0, dec, t, job);
 
-        // Constrained pass from end_state, then the emitting traceback.
-        prev = cost_a;
-        next = cost_b;
-        forward_pass<K>(lab, sx, prev, next, 0, kTile, end_state, 0, dec, t, dec_bits);
-        __threadfence();
-        __syncthreads();
-        if (t == 0)
-            traceback<K>(dec, 0, kTile, end_state, states + tile * kTile, recon + tile * kTile, lut);
-        __syncthreads();
+        // Close the traceback that ran alongside this pass.
+        if (job.kind) {
+            const int jt = job.tile;
+            const int kind = job.kind;
+            finish_job<K>(job, &end_state[jt & 1], t);
+            if (kind == 2) finalize(jt);
+            job.kind = 0;
+        }
+        // This pass's decisions must be complete before any load of them;
+        // writer and readers share one CU, so workgroup scope suffices.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (primer) {
+            const int start = boundary_argmin<K>(boundary_lag ? next : prev, red_v, red_i, t);  // has a barrier
+            if (t == 0) bcast = start;
+            __syncthreads();
+            start_job<K>(job, 1, i, dec, nullptr, context - 1, bcast, t);
+            ++next_p;
+        } else {
+            __syncthreads();
+            start_job<K>(job, 2, i, dec, words[slot], kTile - 1, end_state[slot], t);
+            ++next_f;
+        }
+    }
+    if (job.kind) {
+        const int jt = job.tile;
+        finish_job<K>(job, &end_state[jt & 1], t);
+        finalize(jt);
     }
 }
 
@@ -290,9 +464,9 @@ size_t row_bytes() { return static_cast<size_t>(Geo<K>::kRowBytes); }
 
 size_t workgroup_dec_bytes(int K) {
     switch (K) {
-        case 2: return kTile * row_bytes<2>();
-        case 3: return kTile * row_bytes<3>();
-        case 4: return kTile * row_bytes<4>();
+        case 2: return 2 * kTile * row_bytes<2>();
+        case 3: return 2 * kTile * row_bytes<3>();
+        case 4: return 2 * kTile * row_bytes<4>();
         default: return 0;
     }
 }
@@ -336,15 +510,15 @@ int qsrt_viterbi_tiles(const float* tiles, float* recon, uint16_t* states, int64
     switch (K) {
         case 2:
             hipLaunchKernelGGL(viterbi_tiles_kernel<2>, dim3(grid), dim3(kThreads), 0, stream, tiles, recon, states,
-                               n_tiles, tailbite_context, lut_e4m3, boundary_lag, ws, static_cast<uint32_t>(Geo<2>::kDecBits));
+                               n_tiles, tailbite_context, lut_e4m3, boundary_lag, ws);
             break;
         case 3:
             hipLaunchKernelGGL(viterbi_tiles_kernel<3>, dim3(grid), dim3(kThreads), 0, stream, tiles, recon, states,
-                               n_tiles, tailbite_context, lut_e4m3, boundary_lag, ws, static_cast<uint32_t>(Geo<3>::kDecBits));
+                               n_tiles, tailbite_context, lut_e4m3, boundary_lag, ws);
             break;
         default:
             hipLaunchKernelGGL(viterbi_tiles_kernel<4>, dim3(grid), dim3(kThreads), 0, stream, tiles, recon, states,
-                               n_tiles, tailbite_context, lut_e4m3, boundary_lag, ws, static_cast<uint32_t>(Geo<4>::kDecBits));
+                               n_tiles, tailbite_context, lut_e4m3, boundary_lag, ws);
             break;
     }
     QSRT_HIP_TRY(hipGetLastError());
