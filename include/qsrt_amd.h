@@ -56,6 +56,25 @@ int qsrt_viterbi_tiles(const float *tiles, float *recon, uint16_t *states, int64
                        int tailbite_context, const uint8_t *lut_e4m3, int boundary_lag, void *workspace,
                        size_t workspace_bytes, void *stream);
 
+/*
+ * EXL word packing of n_tiles tiles at rate K (2..4):
+ *   states u16 [n_tiles, 256] (only the low K bits are stored; 16-byte
+ *   aligned), words i16 [n_tiles, 16 K] out.
+ * Replaces the un-vendored ext.pack_trellis called from
+ * qsrt/exl3_encoder_backend.py:2361-2372, whose word order the reference
+ * restates in qsrt/qsrt.py:861-883 (pack_trellis_edges).
+ */
+int qsrt_pack_edges(const uint16_t *states, int64_t n_tiles, int K, int16_t *words, void *stream);
+
+/*
+ * Inverse of qsrt_pack_edges followed by the cyclic state closed form:
+ *   words i16 [n_tiles, 16 K] -> states u16 [n_tiles, 256].
+ * Replaces unpack_trellis_states (qsrt/qsrt.py:910-913) =
+ * unpack_trellis_edges (:886-907) + reconstruct_trellis_states
+ * (qsrt/exl3_reference.py:34-58).
+ */
+int qsrt_unpack_states(const int16_t *words, int64_t n_tiles, int K, uint16_t *states, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,106 @@
+"""Oracle: BlockLDLQ algebra and regularisation in float64 -- test
+infrastructure only.
+
+Restates ``qsrt/exl3_encoder_backend.py``:
+* ``block_ldl`` (:323-393): Cholesky C, L = C blockdiag(C_ii)^-1 -- pinned
+  by L D L^T == H with D = blockdiag(C_ii C_ii^T) and unit diagonal blocks
+  (the check of ``tests/test_blockldlq_proof.py:31-60``);
+* the reverse feedback targets of ``ldlq`` (:420-539): block b is quantized
+  against W_b + sum_{r > b} L_rb^T (W - Q)_r, i.e. T = W + L0^T (W - Q) with
+  L0 the strictly block-lower part -- pinned by the identity
+  T - Q == (I + L0^T)(W - Q) for an arbitrary quantizer
+  (``tests/test_blockldlq_proof.py:62-95``) and by a direct per-block loop;
+* ``regularize`` (:2580-2708) up to the global-scale search and the
+  Hessian congruence of ``_factor_capture_H`` (:2125-2160) -- "parity
+  unpinned" beyond these restatements: no reference test or fixture holds
+  values for them (the reference backend cannot be imported here).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from .fmt import hadamard
+
+CODEBOOK_SCALE = 1.24371088
+
+
+def block_ldl(H: np.ndarray, b: int = 16):
+    """Return (L unit block-lower, D block-diagonal blocks [m, b, b])."""
+
+    H = np.asarray(H, dtype=np.float64)
+    n = H.shape[0]
+    m = n // b
+    C = np.linalg.cholesky(H)
+    blocks = np.stack([C[i * b:(i + 1) * b, i * b:(i + 1) * b] for i in range(m)])
+    L = C.copy()
+    for i in range(m):
+        L[:, i * b:(i + 1) * b] = C[:, i * b:(i + 1) * b] @ np.linalg.inv(blocks[i])
+    for i in range(m):
+        L[i * b:(i + 1) * b, i * b:(i + 1) * b] = np.eye(b)
+    D = np.einsum("mij,mkj->mik", blocks, blocks)
+    return L, D
+
+
+def strictly_block_lower(L: np.ndarray, b: int = 16) -> np.ndarray:
+    L0 = np.array(L, dtype=np.float64, copy=True)
+    for i in range(L0.shape[0] // b):
+        L0[i * b:(i + 1) * b, i * b:(i + 1) * b] = 0.0
+    return L0
+
+
+def feedback_targets(W: np.ndarray, L0: np.ndarray, Q: np.ndarray) -> np.ndarray:
+    """T = W + L0^T (W - Q) (float64)."""
+
+    W = np.asarray(W, dtype=np.float64)
+    return W + np.asarray(L0, dtype=np.float64).T @ (W - np.asarray(Q, dtype=np.float64))
+
+
+def ldlq(W: np.ndarray, L0: np.ndarray, quantize_rows, b: int = 16):
+    """Float64 backward recursion block by block with a caller-supplied
+    quantizer ``quantize_rows(target_rows [16, N], row_block) -> Q rows``."""
+
+    W = np.asarray(W, dtype=np.float64)
+    Q = np.zeros_like(W)
+    targets = np.zeros_like(W)
+    k = W.shape[0]
+    for blk_end in range(k, 0, -b):
+        blk = blk_end - b
+        t = W[blk:blk_end] + L0[blk_end:, blk:blk_end].T @ (W[blk_end:] - Q[blk_end:])
+        targets[blk:blk_end] = t
+        Q[blk:blk_end] = quantize_rows(t, blk // b)
+    return Q, targets
+
+
+def congruence(H: np.ndarray, su_signs: np.ndarray) -> np.ndarray:
+    """Had D_su H D_su Had on 128-blocks (``_factor_capture_H``)."""
+
+    H = np.asarray(H, dtype=np.float64)
+    s = np.asarray(su_signs, dtype=np.float64).reshape(-1)
+    k = H.shape[0]
+    h = hadamard(128)
+    M = (s[:, None] * H) * s[None, :]
+    M = np.einsum("ij,bjn->bin", h, M.reshape(k // 128, 128, k)).reshape(k, k)
+    return np.einsum("kbj,ji->kbi", M.reshape(k, k // 128, 128), h).reshape(k, k)
+
+
+def regularize(weight: np.ndarray, su_signs: np.ndarray, sv_signs: np.ndarray, g_scale: float):
+    """Regularisation with apply_out_scales=False and a fixed global scale:
+    W /= sv; W <- W Had; su = su * rms_rows(W) / -1.24371088 + 1e-10;
+    W /= su; W <- Had W; W *= g; su /= g.  Returns (W, su, sv) in float64."""
+
+    W = np.asarray(weight, dtype=np.float64).copy()
+    k, n = W.shape
+    sv = np.asarray(sv_signs, dtype=np.float64).reshape(1, n)
+    su = np.asarray(su_signs, dtype=np.float64).reshape(k, 1)
+    h = hadamard(128)
+    W /= sv
+    W = np.einsum("kbj,ji->kbi", W.reshape(k, n // 128, 128), h).reshape(k, n)
+    rms = np.sqrt((W * W).mean(axis=1, keepdims=True))
+    rms[np.abs(rms) < 1e-30] = 0.1
+    su = su * rms / (-CODEBOOK_SCALE) + 1e-10
+    W /= su
+    W = np.einsum("ij,bjn->bin", h, W.reshape(k // 128, 128, n)).reshape(k, n)
+    W *= g_scale
+    su = su / g_scale
+    return W, su, sv
