@@ -19,6 +19,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -26,6 +27,8 @@ from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
+
+import torch  # noqa: E402
 
 TILES = 65536
 RATES = (2, 3)
@@ -37,6 +40,148 @@ FP32_PEAK_TFLOPS = 157.3
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# BASELINE configs as seeded synthetic inputs
+# ---------------------------------------------------------------------------
+
+
+def student_t(shape, *, nu: float, std: float, gen: torch.Generator) -> torch.Tensor:
+    """Student-t(nu) from N(0,1) and a chi-square built from nu normals,
+    scaled to standard deviation ``std``."""
+
+    z = torch.randn(shape, generator=gen)
+    chi2 = torch.zeros(shape)
+    for _ in range(int(nu)):
+        chi2 += torch.randn(shape, generator=gen).square()
+    t = z / torch.sqrt(chi2 / nu)
+    return t * (std / math.sqrt(nu / (nu - 2.0)))
+
+
+def ar1_rows(n: int, k: int, rho: float, gen: torch.Generator, device) -> torch.Tensor:
+    """Rows x with x_0 = z_0, x_j = rho x_{j-1} + sqrt(1 - rho^2) z_j (Sigma_ij =
+    rho^|i-j|), built on the device as Z @ T with T the AR(1) Toeplitz factor."""
+
+    z = torch.randn((n, k), generator=gen).to(device)
+    j = torch.arange(k, device=device, dtype=torch.float64)
+    gap = j[None, :] - j[:, None]
+    coef = torch.full((k,), math.sqrt(1.0 - rho * rho), device=device, dtype=torch.float64)
+    coef[0] = 1.0
+    T = torch.where(gap >= 0, coef[:, None] * torch.pow(torch.tensor(rho, device=device, dtype=torch.float64), gap.clamp(min=0)), torch.zeros((), device=device, dtype=torch.float64))
+    return (z.double() @ T).float()
+
+
+def block_wht(x: torch.Tensor, block: int, dim: int) -> torch.Tensor:
+    """Normalised Sylvester Hadamard over ``block``-sized groups of ``dim``."""
+
+    from qsrt_amd.exl3_reference import normalized_hadamard
+
+    h = normalized_hadamard(device=x.device, dtype=torch.float32, size=block)
+    x = x.float().movedim(dim, -1)
+    shape = x.shape
+    y = (x.reshape(*shape[:-1], shape[-1] // block, block) @ h).reshape(shape)
+    return y.movedim(-1, dim).contiguous()
+
+
+def coupled_expert(w_gate, w_up, w_down):
+    """Exact coupled basis with the zero draw (all-ones signs): interleave
+    gate/up rows, Hadamard 512 along hidden and 128 along the interleaved
+    rows; down gets 128 along intermediate and 512 along hidden
+    (reference qsrt/qsrt_coupled.py:145-196)."""
+
+    inter = w_gate.shape[0]
+    inter2 = torch.stack((w_gate, w_up), dim=1).reshape(2 * inter, -1)
+    up = block_wht(block_wht(inter2, 512, 1), 128, 0)
+    down = block_wht(block_wht(w_down, 128, 1), 512, 0)
+    return up[:inter].contiguous(), up[inter:].contiguous(), down
+
+
+def uncoupled_upstream(g_c, u_c):
+    """Inverse of the upstream part of :func:`coupled_expert` (self-inverse
+    Hadamards, then de-interleave)."""
+
+    inter = g_c.shape[0]
+    x = torch.cat((g_c, u_c), dim=0)
+    x = block_wht(block_wht(x, 128, 0), 512, 1)
+    x = x.reshape(inter, 2, -1)
+    return x[:, 0].contiguous(), x[:, 1].contiguous()
+
+
+def run_expert_encode(bits: int = 3, hidden: int = 7168, inter: int = 2048, tokens: int = 16384, rho: float = 0.85, log=print):
+    """BASELINE config 4 at rate ``bits``: one Kimi-class SwiGLU expert in the
+    exact coupled basis, H13 from ``tokens`` AR(1) rows, H2 rebuilt from the
+    reconstructed gate/up SwiGLU activations, all three matrices encoded with
+    BlockLDLQ.  Returns timing and quality figures."""
+
+    from qsrt_amd import exl3_encoder_backend as be
+    from qsrt_amd import qsrt as Q
+    from qsrt_amd.exl3_reference import decode_exl3_weight
+    from qsrt_amd.ldlq import make_shared_h
+    from qsrt_amd.sqg_e4m3 import sqg_xor_cheb_t12_bytes
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator().manual_seed(20261201 + 4)
+    w_gate = student_t((inter, hidden), nu=5, std=0.015, gen=gen).bfloat16().float().to(dev)
+    w_up = student_t((inter, hidden), nu=5, std=0.015, gen=gen).bfloat16().float().to(dev)
+    w_down = student_t((hidden, inter), nu=5, std=0.015, gen=gen).bfloat16().float().to(dev)
+    x = ar1_rows(tokens, hidden, rho, gen, dev)
+    torch.cuda.synchronize()
+    g_c, u_c, d_c = coupled_expert(w_gate, w_up, w_down)
+    h13 = block_wht(block_wht(x.T @ x, 512, 0), 512, 1)  # transform_h13 with unit signs
+    lut = sqg_xor_cheb_t12_bytes(bits)
+    tiles_encoded = [0]
+    real = be.quantize_tiles_multigpu
+
+    def counting(tiles, qa):
+        tiles_encoded[0] += tiles.shape[0]
+        return real(tiles, qa)
+
+    def qargs(seed, sv_seed):
+        return {"K": bits, "seed": seed, "sv_seed": sv_seed, "sigma_reg": 0.01, "devices": [str(dev)],
+                "apply_out_scales": False, "tailbite_context": 128, "sqg_e4m3_lut": lut}
+
+    be.quantize_tiles_multigpu = counting
+    try:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        shared13 = make_shared_h(hidden, dev, h13)
+        shared13["count"] = tokens
+        qa_g, qa_u = qargs(1_000_000, 1_499_979), qargs(1_000_002, 1_499_981)
+        (pg, tg), (pu, tu) = be.quantize_uniform_batch([g_c.T.contiguous(), u_c.T.contiguous()], [shared13, shared13], [qa_g, qa_u])
+        torch.cuda.synchronize()
+        t_upstream = time.perf_counter() - t0
+        # H2 from the reconstructed gate/up activations in the source basis
+        dec = lambda t: decode_exl3_weight(Q.unpack_trellis_states(t["trellis"], bits), t["suh"], t["svh"], bits=bits).T
+        g_hat, u_hat = uncoupled_upstream(dec(tg), dec(tu))
+        h = torch.nn.functional.silu(x @ g_hat.T) * (x @ u_hat.T)
+        h2 = block_wht(block_wht(h.T @ h, 128, 0), 128, 1)  # transform_h2 with unit signs
+        del h
+        shared2 = make_shared_h(inter, dev, h2)
+        shared2["count"] = tokens
+        qa_d = qargs(1_000_001, 1_499_980)
+        t1 = time.perf_counter()
+        _, pd, td = be.quantize_qsrt(d_c.T.contiguous(), shared2, qa_d, False)
+        torch.cuda.synchronize()
+        t_down = time.perf_counter() - t1
+        total = time.perf_counter() - t0
+    finally:
+        be.quantize_tiles_multigpu = real
+    weights = 3 * hidden * inter
+    out = {
+        "bits": bits,
+        "weights": weights,
+        "seconds": total,
+        "seconds_upstream": t_upstream,
+        "seconds_down": t_down,
+        "seconds_h2_rebuild": total - t_upstream - t_down,
+        "M_weights_per_s": weights / total / 1e6,
+        "tile_encodes": tiles_encoded[0],
+        "proxy": {"gate": pg, "up": pu, "down": pd},
+        "g_scale": {"gate": qa_g["g_scale"], "up": qa_u["g_scale"], "down": qa_d["g_scale"]},
+    }
+    log(f"[bench] expert K{bits}: {total:.2f} s ({out['M_weights_per_s']:.1f} M w/s), {tiles_encoded[0]} tile encodes")
+    return out
 
 
 def cpu_baseline(tiles_np, seconds_target: float = 12.0):
