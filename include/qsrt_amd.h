@@ -75,6 +75,23 @@ int qsrt_pack_edges(const uint16_t *states, int64_t n_tiles, int K, int16_t *wor
  */
 int qsrt_unpack_states(const int16_t *words, int64_t n_tiles, int K, uint16_t *states, void *stream);
 
+/*
+ * Blockwise normalised Sylvester-Hadamard rotation, in place, of an FP32
+ * row-major matrix x [rows, cols] with leading dimension ld (elements):
+ *   side 0: each group of `block` rows  r  ->  H_block @ r
+ *   side 1: each group of `block` cols  c  ->  c @ H_block
+ * H_block[i][j] = (-1)^popcount(i & j) / sqrt(block); block 64..512.
+ * Optional device vectors of length rows (side 0) or cols (side 1), NULL
+ * for none, fuse the surrounding scalings:
+ *   x[a] <- post_mul[a] * H(x * pre_mul / pre_div)[a].
+ * x 16-byte aligned; cols and ld multiples of 4.
+ * Replaces preapply_had_l/_r and blockwise_preapply_had_l_/_r_
+ * (qsrt/exl3_encoder_backend.py:275-320) and block_hadamard /
+ * signed_block_hadamard (qsrt/qsrt_coupled.py:49-126).
+ */
+int qsrt_hadamard(float *x, int64_t rows, int64_t cols, int64_t ld, int block, int side, const float *pre_mul,
+                  const float *pre_div, const float *post_mul, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

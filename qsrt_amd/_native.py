@@ -37,6 +37,10 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "qsrt_pack_edges": (_c_int, [_c_void_p, _c_i64, _c_int, _c_void_p, _c_void_p]),
     "qsrt_unpack_states": (_c_int, [_c_void_p, _c_i64, _c_int, _c_void_p, _c_void_p]),
+    "qsrt_hadamard": (
+        _c_int,
+        [_c_void_p, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
+    ),
 }
 
 

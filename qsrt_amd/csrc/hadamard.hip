@@ -1,0 +1,199 @@
+// Blockwise normalised Sylvester-Hadamard rotation of an FP32 matrix, in place.
+//
+// side 0 ("left", reference preapply_had_l / blockwise_preapply_had_l_,
+// qsrt/exl3_encoder_backend.py:275-320): every group of `block` consecutive
+// rows is replaced by H_block @ rows.  side 1 ("right", preapply_had_r):
+// every group of `block` consecutive columns by cols @ H_block.
+// H_block[i][j] = (-1)^popcount(i & j) / sqrt(block), the matrix of
+// exl3_reference.py:210-227 and of the butterfly in qsrt_coupled.py:49-83.
+//
+// Optional vectors indexed along the transformed axis fuse the sign and
+// scale multiplies that surround every rotation in the encoder:
+//   y = post_mul[a] * H(x * pre_mul[a] / pre_div[a])
+// (signed_block_hadamard, qsrt_coupled.py:108-126; the `W /= sv`, `W /= su`
+// of regularize; the `H *= su` congruence; the `* su`, `* sv` of decode).
+//
+// Design: one 256-thread workgroup per 8192-element tile (block x 8192/block
+// of the two axes).  The tile is read with coalesced float4 loads into LDS,
+// transformed in two in-register rounds (bits 0..4 of the transformed
+// index, then the remaining bits), each thread owning one 32- or
+// 2^(log2(block)-5)-point line per round, and written back with float4
+// stores.  The kernel is HBM-bound: 8 bytes per element per call.
+
+#include "common.h"
+#include "qsrt_amd.h"
+
+namespace {
+
+constexpr int kTileElems = 8192;
+constexpr int kThreads = 256;
+
+template <int NB>
+__device__ __forceinline__ void fwht(float (&v)[1 << NB]) {
+#pragma unroll
+    for (int h = 1; h < (1 << NB); h <<= 1) {
+#pragma unroll
+        for (int i = 0; i < (1 << NB); ++i) {
+            if (i & h) continue;
+            const float a = v[i], b = v[i + h];
+            v[i] = a + b;
+            v[i + h] = a - b;
+        }
+    }
+}
+
+// One round over bits [LO, LO + NBITS) of the transformed index a, for every
+// line (other-axis index b, remaining bits of a) of the tile.
+template <int NB, int LO, int NBITS, int S, int O>
+__device__ __forceinline__ void lds_round(float* lds, int t) {
+    constexpr int V = 1 << NBITS;
+    constexpr int kLines = kTileElems / V;
+    static_assert(kLines % kThreads == 0, "line count must fill the workgroup");
+#pragma unroll
+    for (int k = 0; k < kLines / kThreads; ++k) {
+        const int line = t + kThreads * k;
+        const int b = line % O;
+        const int h = line / O;
+        const int base = (h & ((1 << LO) - 1)) | ((h >> LO) << (LO + NBITS));
+        float v[V];
+#pragma unroll
+        for (int j = 0; j < V; ++j) v[j] = lds[(base | (j << LO)) * S + b];
+        fwht<NBITS>(v);
+#pragma unroll
+        for (int j = 0; j < V; ++j) lds[(base | (j << LO)) * S + b] = v[j];
+    }
+}
+
+template <int NB, bool LEFT>
+__global__ __launch_bounds__(kThreads) void hadamard_kernel(float* __restrict__ x, int64_t rows, int64_t cols,
+                                                            int64_t ld, int64_t tiles_b,
+                                                            const float* __restrict__ pre_mul,
+                                                            const float* __restrict__ pre_div,
+                                                            const float* __restrict__ post_mul, float norm) {
+    constexpr int B = 1 << NB;        // transformed extent of one tile
+    constexpr int O = kTileElems / B;  // other-axis extent of one tile
+    constexpr int S = O + 1;           // LDS stride per transformed index (odd: spreads banks)
+    __shared__ float lds[B * S];
+
+    const int t = threadIdx.x;
+    const int64_t tile = blockIdx.x;
+    const int64_t a0 = (tile / tiles_b) * B;
+    const int64_t b0 = (tile % tiles_b) * O;
+    const int64_t ext_b = LEFT ? cols : rows;
+
+    // ---- load (float4 along the contiguous axis), pre-scale, into LDS[a][b]
+#pragma unroll
+    for (int k = 0; k < kTileElems / 4 / kThreads; ++k) {
+        const int f = t + kThreads * k;
+        if constexpr (LEFT) {
+            const int a = f / (O / 4), bq = f % (O / 4);
+            const int64_t col = b0 + 4 * bq;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (col < ext_b) v = *reinterpret_cast<const float4*>(x + (a0 + a) * ld + col);
+            float s = 1.0f;
+            if (pre_mul) s = pre_mul[a0 + a];
+            if (pre_div) {
+                v.x /= pre_div[a0 + a]; v.y /= pre_div[a0 + a];
+                v.z /= pre_div[a0 + a]; v.w /= pre_div[a0 + a];
+            }
+            float* d = lds + a * S + 4 * bq;
+            d[0] = v.x * s; d[1] = v.y * s; d[2] = v.z * s; d[3] = v.w * s;
+        } else {
+            const int b = f / (B / 4), aq = f % (B / 4);
+            const int64_t row = b0 + b;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (row < ext_b) v = *reinterpret_cast<const float4*>(x + row * ld + a0 + 4 * aq);
+            float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t a = a0 + 4 * aq + i;
+                if (pre_mul) e[i] *= pre_mul[a];
+                if (pre_div) e[i] /= pre_div[a];
+                lds[(4 * aq + i) * S + b] = e[i];
+            }
+        }
+    }
+    __syncthreads();
+    lds_round<NB, 0, 5, S, O>(lds, t);
+    __syncthreads();
+    lds_round<NB, 5, NB - 5, S, O>(lds, t);
+    __syncthreads();
+
+    // ---- store: normalise, post-scale, float4 along the contiguous axis
+#pragma unroll
+    for (int k = 0; k < kTileElems / 4 / kThreads; ++k) {
+        const int f = t + kThreads * k;
+        if constexpr (LEFT) {
+            const int a = f / (O / 4), bq = f % (O / 4);
+            const int64_t col = b0 + 4 * bq;
+            if (col >= ext_b) continue;
+            float s = norm;
+            if (post_mul) s *= post_mul[a0 + a];
+            const float* d = lds + a * S + 4 * bq;
+            *reinterpret_cast<float4*>(x + (a0 + a) * ld + col) = make_float4(d[0] * s, d[1] * s, d[2] * s, d[3] * s);
+        } else {
+            const int b = f / (B / 4), aq = f % (B / 4);
+            const int64_t row = b0 + b;
+            if (row >= ext_b) continue;
+            float e[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float s = norm;
+                if (post_mul) s *= post_mul[a0 + 4 * aq + i];
+                e[i] = lds[(4 * aq + i) * S + b] * s;
+            }
+            *reinterpret_cast<float4*>(x + row * ld + a0 + 4 * aq) = make_float4(e[0], e[1], e[2], e[3]);
+        }
+    }
+}
+
+template <int NB>
+int launch(float* x, int64_t rows, int64_t cols, int64_t ld, int side, const float* pre_mul, const float* pre_div,
+           const float* post_mul, hipStream_t stream) {
+    constexpr int B = 1 << NB;
+    constexpr int O = kTileElems / B;
+    const int64_t ext_a = side == 0 ? rows : cols;
+    const int64_t ext_b = side == 0 ? cols : rows;
+    const int64_t tiles_b = (ext_b + O - 1) / O;
+    const int64_t tiles = (ext_a / B) * tiles_b;
+    if (tiles > 0x7fffffff) return qsrt::fail(qsrt::kBadArgument, "matrix too large for one launch");
+    const float norm = 1.0f / sqrtf(static_cast<float>(B));
+    if (side == 0)
+        hipLaunchKernelGGL((hadamard_kernel<NB, true>), dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, stream,
+                           x, rows, cols, ld, tiles_b, pre_mul, pre_div, post_mul, norm);
+    else
+        hipLaunchKernelGGL((hadamard_kernel<NB, false>), dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, stream,
+                           x, rows, cols, ld, tiles_b, pre_mul, pre_div, post_mul, norm);
+    QSRT_HIP_TRY(hipGetLastError());
+    return qsrt::kOk;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qsrt_hadamard(float* x, int64_t rows, int64_t cols, int64_t ld, int block, int side, const float* pre_mul,
+                  const float* pre_div, const float* post_mul, void* stream_handle) {
+    hipStream_t stream = static_cast<hipStream_t>(stream_handle);
+    if (side != 0 && side != 1) return qsrt::fail(qsrt::kBadArgument, "side must be 0 (rows) or 1 (columns)");
+    if (rows < 0 || cols < 0) return qsrt::fail(qsrt::kBadArgument, "negative matrix extent");
+    if (rows == 0 || cols == 0) return qsrt::kOk;
+    if (!x) return qsrt::fail(qsrt::kBadArgument, "null matrix pointer");
+    if (ld < cols) return qsrt::fail(qsrt::kBadArgument, "leading dimension %lld < columns %lld", (long long)ld,
+                                     (long long)cols);
+    if (ld % 4 || cols % 4 || reinterpret_cast<uintptr_t>(x) % 16)
+        return qsrt::fail(qsrt::kBadArgument, "matrix must be 16-byte aligned with columns and ld multiples of 4");
+    const int64_t ext_a = side == 0 ? rows : cols;
+    if (ext_a % block)
+        return qsrt::fail(qsrt::kBadArgument, "Hadamard axis (%lld) must be divisible by block %d", (long long)ext_a,
+                          block);
+    switch (block) {
+        case 64: return launch<6>(x, rows, cols, ld, side, pre_mul, pre_div, post_mul, stream);
+        case 128: return launch<7>(x, rows, cols, ld, side, pre_mul, pre_div, post_mul, stream);
+        case 256: return launch<8>(x, rows, cols, ld, side, pre_mul, pre_div, post_mul, stream);
+        case 512: return launch<9>(x, rows, cols, ld, side, pre_mul, pre_div, post_mul, stream);
+        default: return qsrt::fail(qsrt::kBadArgument, "Hadamard block %d not supported (64, 128, 256, 512)", block);
+    }
+}
+
+}  // extern "C"
