@@ -92,6 +92,47 @@ int qsrt_unpack_states(const int16_t *words, int64_t n_tiles, int K, uint16_t *s
 int qsrt_hadamard(float *x, int64_t rows, int64_t cols, int64_t ld, int block, int side, const float *pre_mul,
                   const float *pre_div, const float *post_mul, void *stream);
 
+/*
+ * One matrix (or one record strip of a mixed-rate matrix) for qsrt_decode.
+ * Tile (r, c) of the [rows/16, cols/16] tile grid starts at
+ *   words + r * tile_row_stride + c * tile_col_stride   (int16 elements)
+ * and holds 16 K int16 EXL words.  Output element (i, j) is written to
+ *   out[i * out_ld + j] = row_scale[i] * col_scale[j] * (H X H)[i][j]
+ * with H the unnormalised 128-block +-1 Sylvester Hadamard (pass
+ * row_scale = su / 128 to reproduce the normalised decode).
+ */
+typedef struct qsrt_decode_job {
+    const int16_t *words;
+    int64_t tile_row_stride;
+    int64_t tile_col_stride;
+    const float *row_scale;
+    const float *col_scale;
+    void *out;
+    int64_t out_ld;
+    int64_t rows;
+    int64_t cols;
+} qsrt_decode_job;
+
+/* Device workspace bytes qsrt_decode needs for n_jobs jobs. */
+size_t qsrt_decode_workspace_bytes(int n_jobs);
+
+/*
+ * Fused decode of packed trellis payloads at rate K (2..4) to bf16
+ * (out_dtype 0) or f32 (out_dtype 1):
+ *   words -> cyclic 16-bit states -> lut_e4m3[state] -> X (tensor-core
+ *   order inside each 16x16 tile) -> row_scale . H128 X H128 . col_scale.
+ * `jobs` is a HOST array (copied to `workspace` on `stream`); rows and cols
+ * multiples of 128; words 4-byte aligned with even strides; out 8-byte
+ * (bf16) / 16-byte (f32) aligned; out_ld % 4 == 0; col_scale 16-byte
+ * aligned.  exact_fp8 != 0 selects the FP8 matrix-core path, exact for
+ * LUTs with |label| <= 6 (every SQG table); 0 the FP32 path (any LUT).
+ * Replaces decode_exl3_weight / decode_qsrt_weight
+ * (qsrt/exl3_reference.py:61-330) and decode_qsrt_exl3_weight
+ * (qsrt/qsrt.py:1175-1209).
+ */
+int qsrt_decode(const qsrt_decode_job *jobs, int n_jobs, int K, const uint8_t *lut_e4m3, int exact_fp8,
+                int out_dtype, void *workspace, size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

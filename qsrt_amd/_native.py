@@ -37,11 +37,29 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "qsrt_pack_edges": (_c_int, [_c_void_p, _c_i64, _c_int, _c_void_p, _c_void_p]),
     "qsrt_unpack_states": (_c_int, [_c_void_p, _c_i64, _c_int, _c_void_p, _c_void_p]),
+    "qsrt_decode_workspace_bytes": (_c_size, [_c_int]),
+    "qsrt_decode": (_c_int, [_c_void_p, _c_int, _c_int, _c_void_p, _c_int, _c_int, _c_void_p, _c_size, _c_void_p]),
     "qsrt_hadamard": (
         _c_int,
         [_c_void_p, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
     ),
 }
+
+
+class DecodeJob(ctypes.Structure):
+    """``qsrt_decode_job`` of ``include/qsrt_amd.h``."""
+
+    _fields_ = [
+        ("words", _c_void_p),
+        ("tile_row_stride", _c_i64),
+        ("tile_col_stride", _c_i64),
+        ("row_scale", _c_void_p),
+        ("col_scale", _c_void_p),
+        ("out", _c_void_p),
+        ("out_ld", _c_i64),
+        ("rows", _c_i64),
+        ("cols", _c_i64),
+    ]
 
 
 class NativeError(RuntimeError):

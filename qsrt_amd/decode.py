@@ -1,0 +1,124 @@
+"""Fused trellis decode on MI355X: packed EXL words -> bf16 (or f32) weights.
+
+``decode_words`` decodes one uniform-rate ``[K/16, N/16, 16 bits]`` trellis
+(the ``trellis`` tensor of ``quantize_qsrt``); ``decode_packed`` decodes a
+mixed-rate ``PackedQSRTTrellis`` payload record by record with one launch per
+rate.  Both compute ``W = H_R(H_L(X) * su) * sv`` (reference
+``qsrt/exl3_reference.py:280-330``, ``qsrt/qsrt.py:1175-1209``) in the HIP
+kernel behind ``qsrt_decode`` (``include/qsrt_amd.h``).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _native
+from .sqg_quantizer import _lut_abs_max
+
+# FP8 matrix-core products are exact for labels up to this magnitude (every
+# SQG table: |label| <= 5.5); larger tables use the FP32 path.
+FP8_EXACT_MAX_LABEL = 6.0
+_OUT = {torch.bfloat16: 0, torch.float32: 1}
+
+
+def _check_lut(lut: torch.Tensor, device) -> torch.Tensor:
+    if lut.dtype != torch.uint8 or lut.numel() != 1 << 16:
+        raise ValueError("decode LUT must be uint8[65536] E4M3 bytes")
+    lut = lut.reshape(-1).to(device).contiguous()
+    if lut.data_ptr() % 16:
+        lut = lut.clone()
+    return lut
+
+
+def _scale(v: torch.Tensor, n: int, device, divide: float = 1.0) -> torch.Tensor:
+    if v.ndim != 1 or v.numel() != n:
+        raise ValueError(f"scale vector must contain exactly {n} values")
+    return (v.to(device=device, dtype=torch.float32) / divide).contiguous()
+
+
+def _run(jobs: list, bits: int, lut: torch.Tensor, out_dtype, device) -> None:
+    if not jobs:
+        return
+    lib = _native.lib()
+    arr = (_native.DecodeJob * len(jobs))(*jobs)
+    need = int(lib.qsrt_decode_workspace_bytes(len(jobs)))
+    ws = torch.empty(max(need, 16), dtype=torch.uint8, device=device)
+    exact_fp8 = int(_lut_abs_max(lut) <= FP8_EXACT_MAX_LABEL)
+    _native.check(
+        lib.qsrt_decode(ctypes.cast(arr, ctypes.c_void_p), len(jobs), bits, lut.data_ptr(), exact_fp8,
+                        _OUT[out_dtype], ws.data_ptr(), ws.numel(), _native.stream_handle(device)),
+        "qsrt_decode",
+    )
+
+
+def decode_words(words: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor, bits: int, lut: torch.Tensor, *,
+                 out_dtype=torch.bfloat16, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``[K/16, N/16, 16 bits]`` int16 EXL words + ``suh [K]``, ``svh [N]`` ->
+    ``[K, N]`` weights in ``out_dtype`` (bf16 or f32)."""
+
+    if not words.is_cuda:
+        raise ValueError("decode_words runs on the GPU; move the payload to a CUDA device")
+    if words.dtype != torch.int16 or words.ndim != 3 or words.shape[2] != 16 * bits:
+        raise ValueError("words must be int16 [K/16, N/16, 16 * bits]")
+    if out_dtype not in _OUT:
+        raise ValueError("out_dtype must be torch.bfloat16 or torch.float32")
+    kt, nt, _ = words.shape
+    k, n = 16 * kt, 16 * nt
+    if k % 128 or n % 128:
+        raise ValueError("decode needs K and N multiples of 128")
+    dev = words.device
+    words = words.contiguous()
+    lut = _check_lut(lut, dev)
+    su = _scale(suh, k, dev, 128.0)
+    sv = _scale(svh, n, dev)
+    if out is None:
+        out = torch.empty((k, n), dtype=out_dtype, device=dev)
+    elif out.shape != (k, n) or out.dtype != out_dtype or out.stride(1) != 1:
+        raise ValueError("out must be a row-major [K, N] tensor of out_dtype")
+    job = _native.DecodeJob(words.data_ptr(), nt * 16 * bits, 16 * bits, su.data_ptr(), sv.data_ptr(),
+                            out.data_ptr(), out.stride(0), k, n)
+    _run([job], bits, lut, out_dtype, dev)
+    return out
+
+
+def decode_packed(packed, suh: torch.Tensor, svh: torch.Tensor, luts_by_bits: dict, *, out_dtype=torch.bfloat16,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """Mixed-rate ``PackedQSRTTrellis`` -> ``[K, N]`` weights: every 128-channel
+    record along the rate axis is one decode job at its own rate."""
+
+    from .qsrt import TILE_CHANNELS, TILES_PER_RECORD_AXIS, record_bits
+
+    packed.validate()
+    d = packed.descriptor
+    payload = packed.payload
+    if not payload.is_cuda:
+        raise ValueError("decode_packed runs on the GPU; move the payload to a CUDA device")
+    dev = payload.device
+    k, n = d.k_tiles * TILE_CHANNELS, d.n_tiles * TILE_CHANNELS
+    su = _scale(suh, k, dev, 128.0)
+    sv = _scale(svh, n, dev)
+    if out is None:
+        out = torch.empty((k, n), dtype=out_dtype, device=dev)
+    elif out.shape != (k, n) or out.dtype != out_dtype or out.stride(1) != 1:
+        raise ValueError("out must be a row-major [K, N] tensor of out_dtype")
+    esize = out.element_size()
+    by_bits: dict[int, list] = {}
+    cursor = 0
+    base = payload.data_ptr()
+    for record, bits in enumerate(record_bits(d.mode)):
+        r0 = record * TILES_PER_RECORD_AXIS * TILE_CHANNELS
+        if d.rate_axis == "k":
+            job = _native.DecodeJob(base + 2 * cursor, d.n_tiles * 16 * bits, 16 * bits, su.data_ptr() + 4 * r0,
+                                    sv.data_ptr(), out.data_ptr() + esize * r0 * out.stride(0), out.stride(0), 128, n)
+        else:
+            job = _native.DecodeJob(base + 2 * cursor, TILES_PER_RECORD_AXIS * 16 * bits, 16 * bits, su.data_ptr(),
+                                    sv.data_ptr() + 4 * r0, out.data_ptr() + esize * r0, out.stride(0), k, 128)
+        by_bits.setdefault(bits, []).append(job)
+        cursor += d.tiles_per_record * 16 * bits
+    if cursor != payload.numel():
+        raise ValueError("QSRT trellis payload has trailing data")
+    for bits, jobs in sorted(by_bits.items()):
+        _run(jobs, bits, _check_lut(luts_by_bits[bits], dev), out_dtype, dev)
+    return out
