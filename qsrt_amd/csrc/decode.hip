@@ -7,31 +7,39 @@
 //   W        = H_R( H_L(X) * su[:, None] ) * sv[None, :]
 // with H_L / H_R the normalised 128-block Sylvester Hadamards.  Row scaling
 // commutes with the right product, so per 128x128 block
-//   W_blk = su . (H128 X_blk H128) . sv / 128   (unnormalised +-1 Hadamards).
-// H128 = H8 (x) H16 (Kronecker over the 8x8 tiles of the block and the 16x16
-// positions in a tile), so the block transform factors into per-tile H16
-// products on the matrix cores and 8-point butterflies across tiles.
+//   W_blk = su . (H128 X_blk H128) . sv / 128   (unnormalised +-1 Hadamards)
+// and H128 = H8 (x) H16 (Kronecker over the 8x8 tiles of a block and the
+// 16x16 positions of a tile).
 //
-// Per workgroup (8 waves), per block:
-//  1. wave w owns tile-column w.  Lane (c = lane % 16, g = lane / 16) holds,
-//     for every tile, the 4 values of column c at rows 2g + {0,1,8,9}: the
-//     four consecutive trellis positions 32 (c % 8) + 8 g + 4 (c / 8) + 0..3
-//     (tensor-core order), i.e. one 16 + 3K-bit window of the tile's
-//     MSB-first bitstream.  EXL stores adjacent 16-bit words swapped, so a
-//     little-endian u32 read is the big-endian 32-bit chunk of the stream.
-//  2. labels come from the state-indexed E4M3 LUT in LDS and are used as fp8
-//     MFMA operands directly: A = [X_a ; X_(a+1)]^T (k = the 32 rows of two
-//     vertically adjacent tiles), B = [H16 ; +-H16]: the two products are
-//     (X_a +- X_(a+1))^T H16 -- the per-tile left H16 fused with the first
-//     H8 butterfly stage across tile-rows (bit 0 of a).
-//     (fp8 MFMA sums are exact for |label| <= 6; larger tables take the
-//     FP32-MFMA variant below.)
-//  3. the other two H8 stages across tile-rows on VALU; multiply by su/128.
-//  4. right H16 per tile on FP32 MFMA (16x16x4, +-1 operands): exact
-//     products.  Output lane layout = row c, columns 4g..4g+3 of the tile.
-//  5. exchange through LDS (wave w now owns tile-row w), H8 across
-//     tile-columns on VALU, multiply by sv, convert, store 4 consecutive
-//     outputs per lane per tile.
+// Per workgroup (8 waves, two workgroups per CU), per block:
+//  A. wave w decodes tile-column w.  Lane (c = lane % 16, g = lane / 16)
+//     takes, in every tile, the 4 values of column c at rows 2g + {0,1,8,9}:
+//     trellis positions 32 (c % 8) + 8 g + 4 (c / 8) + 0..3 (tensor-core
+//     order), one 16 + 3K-bit window of the tile's MSB-first bitstream (EXL
+//     stores adjacent 16-bit words swapped, so a little-endian u32 read is the
+//     big-endian 32-bit chunk of the stream).  Labels come from the
+//     state-indexed E4M3 LUT in LDS; the lane's 32 labels of the tile-column
+//     (8 tiles x 4 rows) are written to a 16 KB LDS label area.
+//  B. wave w produces output tile-row w.  For each tile-column a', the whole
+//     left transform (H8 (x) H16 over the 128 rows) is ONE fp8 MFMA
+//     (16x16x128): A = the lane's 32 labels of that tile-column, B = +-1 with
+//     B[(a, row)][col] = H8[w][a] H16[row][col].  Exact for |label| <= 6 (sums
+//     of at most 128 x 6 on multiples of 2^-9).  The eight results of the
+//     tile-row stay in registers; the right H8 across tile-columns runs on
+//     VALU (exact: < 2^22 units of 2^-9).  Each value is split into fp16
+//     hi + lo (exact, 11 + 11 bits), and the right H16 is one f16 MFMA
+//     (16x16x32) per tile with k = [hi ; lo] and A = [H16 ; H16] with row i
+//     scaled by the fp16 sv of output column i.  Finally times su/128,
+//     conversion, four consecutive outputs per lane per tile.
+//  Memory traffic is shaped for the vector-memory pipe: a wave's 8 tiles of
+//  packed words arrive with one 16-byte load per lane and are staged through
+//  the wave's own slice of the LDS label area; outputs are staged through the
+//  same slice (XOR-swizzled 16-byte chunks) so each store instruction writes
+//  full 128-byte row segments.  Words, su and sv of the next block are loaded
+//  before this block's stores (vector-memory counters retire in issue order,
+//  so a load issued after a store would wait for the store to drain).
+// Tables whose labels exceed 6 in magnitude use FP32 MFMAs for both products
+// (labels widened exactly to FP32), with the same data movement.
 
 #include "common.h"
 #include "qsrt_amd.h"
@@ -39,10 +47,14 @@
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(1))) uint32_t* gu32;
+typedef const __attribute__((address_space(1))) float* gf32;
+typedef const __attribute__((address_space(1))) f32x4* gf4;
 
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kXchFloat4 = 8 * 8 * 64;  // 64 tiles x 64 lanes x float4
+constexpr int kLabelBytes = 64 * 256;  // one byte per weight of a block
 
 __device__ __forceinline__ int hsign(int i, int j) { return (__builtin_popcount(i & j) & 1) ? -1 : 1; }
 
@@ -59,61 +71,99 @@ struct Job {
     int64_t first_block;  // prefix over jobs (filled by the host)
 };
 
-template <typename OutT>
-__device__ __forceinline__ void store4(OutT* p, float a, float b, float c, float d);
+struct BlockCtx {
+    const int16_t* words;  // tile (8 br, 8 bc) of the block
+    int64_t trs, tcs;
+    const float* su;       // row 128 br
+    const float* sv;       // col 128 bc
+    char* out;             // element (128 br, 128 bc)
+    int64_t ld;
+};
 
-template <>
-__device__ __forceinline__ void store4<float>(float* p, float a, float b, float c, float d) {
-    *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
+__device__ __forceinline__ BlockCtx block_ctx(const Job* jobs, int n_jobs, int& j, int64_t blk, int out_size) {
+    while (j + 1 < n_jobs && jobs[j + 1].first_block <= blk) ++j;
+    const Job& J = jobs[j];
+    const int64_t local = blk - J.first_block;
+    const int64_t nbc = J.cols >> 7;
+    const int64_t br = local / nbc, bc = local - br * nbc;
+    BlockCtx x;
+    x.words = J.words + 8 * br * J.tile_row_stride + 8 * bc * J.tile_col_stride;
+    x.trs = J.tile_row_stride;
+    x.tcs = J.tile_col_stride;
+    x.su = J.row_scale + 128 * br;
+    x.sv = J.col_scale + 128 * bc;
+    x.out = static_cast<char*>(J.out) + (128 * br * J.out_ld + 128 * bc) * out_size;
+    x.ld = J.out_ld;
+    return x;
 }
 
-template <>
-__device__ __forceinline__ void store4<__bf16>(__bf16* p, float a, float b, float c, float d) {
-    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-    bf16x4 v = {static_cast<__bf16>(a), static_cast<__bf16>(b), static_cast<__bf16>(c), static_cast<__bf16>(d)};
-    *reinterpret_cast<bf16x4*>(p) = v;
-}
-
-// 16-bit states of trellis positions p0..p0+3 of one tile from its u32 stream.
+// 16 bytes of the wave's tile-column: lane l < 16 K loads chunk l % (2 K) of
+// tile-row l / (2 K) (each tile is 32 K bytes of words).
 template <int K>
-__device__ __forceinline__ uint32_t window(const uint32_t* u, int m0, int m1, int sh) {
-    const uint64_t two = (static_cast<uint64_t>(u[m0]) << 32) | u[m1];
-    return static_cast<uint32_t>(two >> (32 - sh));
+__device__ __forceinline__ u32x4 fetch_words(const BlockCtx& x, int w, int lane) {
+    if (lane >= 16 * K) return u32x4{0u, 0u, 0u, 0u};
+    const int a = lane / (2 * K), q = lane % (2 * K);
+    const int16_t* tile = x.words + a * x.trs + w * x.tcs;
+    return *(const __attribute__((address_space(1))) u32x4*)(tile + 8 * q);
 }
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 template <int K, bool FP8, typename OutT>
-__global__ __launch_bounds__(kThreads, 1) void decode_kernel(const Job* __restrict__ jobs, int n_jobs,
-                                                             int64_t total_blocks, const uint8_t* __restrict__ lut) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
+void decode_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t total_blocks, const uint8_t* __restrict__ lut) {
+    static_assert(sizeof(OutT) == 2 || sizeof(OutT) == 4, "bf16 or f32 output");
     __shared__ __attribute__((aligned(16))) uint8_t lut_s[65536];
-    __shared__ f32x4 xch[kXchFloat4];
+    // Label area, 2 KB per wave.  During B1: labels of tile-column a', lane l,
+    // half h (tile-rows 4h..4h+3) at ((a' * 2 + h) * 64 + l) * 16.  Wave w's
+    // slice [2 KB w, 2 KB (w + 1)) also stages its packed words (phase A) and
+    // its outputs (phase B2), when no other wave reads it.
+    __shared__ __attribute__((aligned(16))) uint8_t labels[kLabelBytes];
 
     for (int i = threadIdx.x; i < 65536 / 16; i += kThreads)
         reinterpret_cast<uint4*>(lut_s)[i] = reinterpret_cast<const uint4*>(lut)[i];
 
     const int lane = threadIdx.x & 63;
-    const int w = threadIdx.x >> 6;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15;
     const int g = lane >> 4;
     const int rho[4] = {2 * g, 2 * g + 1, 2 * g + 8, 2 * g + 9};
 
-    // fp8 +-1 operands of the left products: B[k = (g, j)][c] = H16[rho(j & 3)][c] (* -1 for j >= 4 in diff)
-    uint64_t b_sum = 0, b_diff = 0;
-    // FP32 operands for the left products of the FP32 variant: lane (c, g) holds H16[rho][c] for its rows
-    float hl[4];
+    // Left-product B operand (fp8 +-1): byte j <-> tile-row j / 4, row rho(j % 4); value H8[w][j/4] H16[rho][c].
+    i32x8 bl;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int s = hsign(rho[j & 3], c);
-        const uint64_t pos = 0x38, neg = 0xB8;  // E4M3 +1 / -1
-        b_sum |= (s > 0 ? pos : neg) << (8 * j);
-        b_diff |= ((j < 4 ? s : -s) > 0 ? pos : neg) << (8 * j);
-        if (j < 4) hl[j] = static_cast<float>(s);
+    for (int r = 0; r < 8; ++r) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int j = 4 * r + b;
+            const int s = hsign(w, j >> 2) * hsign(rho[j & 3], c);
+            v |= (s > 0 ? 0x38u : 0xB8u) << (8 * b);  // E4M3 +1 / -1
+        }
+        bl[r] = static_cast<int>(v);
     }
-    // A operands of the right product: A_q[i = c][k = g] = H16[c][4g + q]
+    // Right-product A operand rows: H16[c][4g + q]
     float hr[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) hr[q] = static_cast<float>(hsign(c, 4 * g + q));
+    float hl[4];  // FP32 path: H16[rho(i)][c]
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hl[i] = static_cast<float>(hsign(rho[i], c));
+    // fp16 sign masks of H16[c][4g + q], q = 0..3, as two packed pairs
+    uint32_t hsg[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+        hsg[h] = (hr[2 * h] < 0.f ? 0x8000u : 0u) | (hr[2 * h + 1] < 0.f ? 0x80000000u : 0u);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) asm volatile("" : "+v"(hsg[h]));
+    // Keep the operand constants in registers instead of recomputing them in the loop.
+#pragma unroll
+    for (int r = 0; r < 8; ++r) asm volatile("" : "+v"(bl[r]));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) asm volatile("" : "+v"(hr[q]));
 
-    // bit window of this lane's four positions
     const int p0 = 32 * (c & 7) + 8 * g + 4 * (c >> 3);
     int b0 = (p0 + 1) * K - 16;
     if (b0 < 0) b0 += 256 * K;
@@ -121,90 +171,86 @@ __global__ __launch_bounds__(kThreads, 1) void decode_kernel(const Job* __restri
     const int m1 = (m0 + 1) % (8 * K);
     const int sh = b0 & 31;
 
+    uint8_t* slice = labels + 2048 * w;
+    uint4* lab_w = reinterpret_cast<uint4*>(labels) + (w * 2) * 64 + lane;
+    const uint4* lab_r = reinterpret_cast<const uint4*>(labels) + lane;
+    const uint32_t* wstage = reinterpret_cast<const uint32_t*>(slice);
+
+    int job = 0;
+    int64_t blk = blockIdx.x;
+    u32x4 words = {0u, 0u, 0u, 0u};
+    float su = 0.f, sv[8];
+    BlockCtx ctx{};
+    if (blk < total_blocks) {
+        ctx = block_ctx(jobs, n_jobs, job, blk, sizeof(OutT));
+        words = fetch_words<K>(ctx, w, lane);
+        su = ((gf32)ctx.su)[16 * w + c];
+#pragma unroll
+        for (int a = 0; a < 8; ++a) sv[a] = ((gf32)ctx.sv)[16 * a + c];
+    }
     __syncthreads();
 
-    for (int64_t blk = blockIdx.x; blk < total_blocks; blk += gridDim.x) {
-        // job containing blk (uniform across the workgroup)
-        int lo = 0, hi = n_jobs - 1;
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (jobs[mid].first_block <= blk) lo = mid; else hi = mid - 1;
-        }
-        const Job& J = jobs[lo];
-        const int64_t local = blk - J.first_block;
-        const int64_t nbc = J.cols >> 7;
-        const int64_t br = local / nbc, bc = local - br * nbc;
-
-        // ---- phase 1: tile-column w of the block
-        f32x4 d[8];
-        uint8_t lab[8][4];
+    for (; blk < total_blocks; blk += gridDim.x) {
+        // ---- A: stage the tile-column's words, decode the lane's labels
+        if (lane < 16 * K) reinterpret_cast<u32x4*>(slice)[lane] = words;
+        uint32_t lab[8];
 #pragma unroll
         for (int a = 0; a < 8; ++a) {
-            const uint32_t* u = reinterpret_cast<const uint32_t*>(
-                J.words + (8 * br + a) * J.tile_row_stride + (8 * bc + w) * J.tile_col_stride);
-            const uint32_t win = window<K>(u, m0, m1, sh);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) lab[a][i] = lut_s[(win >> (16 - i * K)) & 0xFFFFu];
+            const uint32_t lo = wstage[a * 8 * K + m0], hi = wstage[a * 8 * K + m1];
+            const uint64_t two = (static_cast<uint64_t>(lo) << 32) | hi;
+            const uint32_t win = static_cast<uint32_t>(two >> (32 - sh));
+            const uint32_t v01 = lut_s[(win >> 16) & 0xFFFFu] | (static_cast<uint32_t>(lut_s[(win >> (16 - K)) & 0xFFFFu]) << 16);
+            const uint32_t v23 = lut_s[(win >> (16 - 2 * K)) & 0xFFFFu] |
+                                 (static_cast<uint32_t>(lut_s[(win >> (16 - 3 * K)) & 0xFFFFu]) << 16);
+            lab[a] = __builtin_amdgcn_perm(v23, v01, 0x06040200u);
         }
-        if constexpr (FP8) {
+        lab_w[0] = make_uint4(lab[0], lab[1], lab[2], lab[3]);
+        lab_w[64] = make_uint4(lab[4], lab[5], lab[6], lab[7]);
+        // ---- prefetch the next block (before this block's stores)
+        const BlockCtx cur = ctx;
+        const float su_cur = su;
+        float sv_cur[8];
 #pragma unroll
-            for (int a = 0; a < 8; a += 2) {
-                uint64_t av = 0;
+        for (int a = 0; a < 8; ++a) sv_cur[a] = sv[a];
+        const int64_t nb = blk + gridDim.x;
+        if (nb < total_blocks) {
+            ctx = block_ctx(jobs, n_jobs, job, nb, sizeof(OutT));
+            words = fetch_words<K>(ctx, w, lane);
+            su = ((gf32)ctx.su)[16 * w + c];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    av |= static_cast<uint64_t>(lab[a][i]) << (8 * i);
-                    av |= static_cast<uint64_t>(lab[a + 1][i]) << (8 * (i + 4));
-                }
-                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                d[a] = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(static_cast<long>(av), static_cast<long>(b_sum), z, 0, 0, 0);
-                d[a + 1] = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(static_cast<long>(av), static_cast<long>(b_diff), z, 0, 0, 0);
-            }
-        } else {
-            // D1 = X^T H16 as four rank-4 FP32 products per tile, then the bit-0 butterfly.
-#pragma unroll
-            for (int a = 0; a < 8; ++a) {
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    // A[c][k = g] = X[rho(i)][c]; B[k = g][col] = H16[rho(i)][col]
-                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qsrt::e4m3_to_float(lab[a][i]), hl[i], acc, 0, 0, 0);
-                }
-                d[a] = acc;
-            }
-#pragma unroll
-            for (int a = 0; a < 8; a += 2) {
-                const f32x4 x = d[a], y = d[a + 1];
-                d[a] = x + y;
-                d[a + 1] = x - y;
-            }
-        }
-        // H8 stages on bits 1 and 2 of the tile-row index
-#pragma unroll
-        for (int h = 2; h < 8; h <<= 1) {
-#pragma unroll
-            for (int a = 0; a < 8; ++a) {
-                if (a & h) continue;
-                const f32x4 x = d[a], y = d[a + h];
-                d[a] = x + y;
-                d[a + h] = x - y;
-            }
-        }
-        // su / 128 of output row 16 a + c; right H16 on FP32 MFMA
-#pragma unroll
-        for (int a = 0; a < 8; ++a) {
-            const float su = J.row_scale[128 * br + 16 * a + c];
-            const f32x4 v = d[a] * su;
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(hr[q], v[q], acc, 0, 0, 0);
-            xch[(a * 8 + w) * 64 + lane] = acc;
+            for (int a = 0; a < 8; ++a) sv[a] = ((gf32)ctx.sv)[16 * a + c];
         }
         __syncthreads();
 
-        // ---- phase 2: tile-row w of the block
+        // ---- B1: output tile-row w, left transform per tile-column
         f32x4 e[8];
 #pragma unroll
-        for (int a = 0; a < 8; ++a) e[a] = xch[(w * 8 + a) * 64 + lane];
+        for (int a2 = 0; a2 < 8; ++a2) {
+            const uint4 x0 = lab_r[(a2 * 2) * 64], x1 = lab_r[(a2 * 2 + 1) * 64];
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            if constexpr (FP8) {
+                const i32x8 av = {static_cast<int>(x0.x), static_cast<int>(x0.y), static_cast<int>(x0.z),
+                                  static_cast<int>(x0.w), static_cast<int>(x1.x), static_cast<int>(x1.y),
+                                  static_cast<int>(x1.z), static_cast<int>(x1.w)};
+                // format 0 = E4M3 for A and B; E8M0 scales 127 = 1.0
+                acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bl, acc, 0, 0, 0, 127, 0, 127);
+            } else {
+                const uint32_t words8[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                for (int a = 0; a < 8; ++a) {
+                    const float sgn = static_cast<float>(hsign(w, a));
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float x = sgn * qsrt::e4m3_to_float((words8[a] >> (8 * i)) & 0xFFu);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x, hl[i], acc, 0, 0, 0);
+                    }
+                }
+            }
+            e[a2] = acc;
+        }
+        __syncthreads();  // every wave is done reading labels: slices are private again
+
+        // ---- B2: right H8 across tile-columns (exact on the fp8 path)
 #pragma unroll
         for (int h = 1; h < 8; h <<= 1) {
 #pragma unroll
@@ -215,15 +261,64 @@ __global__ __launch_bounds__(kThreads, 1) void decode_kernel(const Job* __restri
                 e[a + h] = x - y;
             }
         }
-        OutT* out = static_cast<OutT*>(J.out);
-        const int64_t row = 128 * br + 16 * w + c;
+        // right H16 per tile (sv folded into the rows of A), su/128, stage, store
+        constexpr int kRowBytes = 128;                                     // 16 rows x 128 B = the 2 KB slice
+        constexpr int kChunks = kRowBytes / 16;                            // 16-byte chunks per staged row
+        constexpr int kTilesPerRound = kRowBytes / (16 * static_cast<int>(sizeof(OutT)));  // 4 bf16, 2 f32
+        constexpr int kRounds = 8 / kTilesPerRound;
+        char* out_row0 = cur.out + (16 * w) * cur.ld * sizeof(OutT);
 #pragma unroll
-        for (int a = 0; a < 8; ++a) {
-            const int64_t col = 128 * bc + 16 * a + 4 * g;
-            const float4 sv = *reinterpret_cast<const float4*>(J.col_scale + col);
-            store4<OutT>(out + row * J.out_ld + col, e[a][0] * sv.x, e[a][1] * sv.y, e[a][2] * sv.z, e[a][3] * sv.w);
+        for (int rd = 0; rd < kRounds; ++rd) {
+#pragma unroll
+            for (int t = 0; t < kTilesPerRound; ++t) {
+                const int a = rd * kTilesPerRound + t;
+                f32x4 d = {0.f, 0.f, 0.f, 0.f};
+                if constexpr (FP8) {
+                    // exact split: hi keeps the top 11 significant bits (low 13 mantissa bits cleared),
+                    // lo = e - hi has at most 11 (e is a multiple of 2^-9 below 2^13)
+                    f16x8 bv;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float ev = e[a][q];
+                        const float hi32 = __uint_as_float(__float_as_uint(ev) & 0xFFFFE000u);
+                        bv[q] = static_cast<_Float16>(hi32);
+                        bv[q + 4] = static_cast<_Float16>(ev - hi32);
+                    }
+                    // A rows: +-sv of the output column (sign bits from H16 via XOR)
+                    const uint32_t sv2 = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(sv_cur[a]), static_cast<_Float16>(sv_cur[a])});
+                    const uint32_t a01 = sv2 ^ hsg[0], a23 = sv2 ^ hsg[1];
+                    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+                    const u32x4v araw = {a01, a23, a01, a23};
+                    const f16x8 avh = __builtin_bit_cast(f16x8, araw);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(avh, bv, d, 0, 0, 0);
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        d = __builtin_amdgcn_mfma_f32_16x16x4f32(hr[q] * sv_cur[a], e[a][q], d, 0, 0, 0);
+                }
+                d = d * su_cur;
+                // row c, staged columns 16 t + 4 g .. +3 -> byte offset, 16-byte chunks XOR-swizzled by row
+                const int byte = (16 * t + 4 * g) * static_cast<int>(sizeof(OutT));
+                const int chunk = (byte >> 4) ^ (c & (kChunks - 1));
+                char* dst = reinterpret_cast<char*>(slice) + c * kRowBytes + chunk * 16 + (byte & 15);
+                if constexpr (sizeof(OutT) == 2) {
+                    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+                    const bf16x4 o = {static_cast<__bf16>(d[0]), static_cast<__bf16>(d[1]), static_cast<__bf16>(d[2]),
+                                      static_cast<__bf16>(d[3])};
+                    *reinterpret_cast<bf16x4*>(dst) = o;
+                } else {
+                    *reinterpret_cast<f32x4*>(dst) = d;
+                }
+            }
+            // 16 rows x kRowBytes: lane -> (row, chunk), 16 bytes each
+#pragma unroll
+            for (int r0 = 0; r0 < 16; r0 += 64 / kChunks) {
+                const int row = r0 + lane / kChunks, chunk = lane % kChunks;
+                const u32x4 v = *reinterpret_cast<const u32x4*>(slice + row * kRowBytes + ((chunk ^ (row & (kChunks - 1))) * 16));
+                char* dst = out_row0 + row * cur.ld * sizeof(OutT) + rd * kRowBytes + chunk * 16;
+                *(__attribute__((address_space(1))) u32x4*)dst = v;
+            }
         }
-        __syncthreads();
     }
 }
 
@@ -258,7 +353,6 @@ int qsrt_decode(const qsrt_decode_job* jobs, int n_jobs, int K, const uint8_t* l
                           qsrt_decode_workspace_bytes(n_jobs));
     if (reinterpret_cast<uintptr_t>(lut_e4m3) % 16 || reinterpret_cast<uintptr_t>(workspace) % 16)
         return qsrt::fail(qsrt::kBadArgument, "LUT and workspace must be 16-byte aligned");
-    const size_t out_align = out_dtype == 0 ? 8 : 16;
     Job* host = static_cast<Job*>(malloc(sizeof(Job) * n_jobs));
     if (!host) return qsrt::fail(qsrt::kHipError, "host allocation failed");
     int64_t total = 0;
@@ -266,14 +360,15 @@ int qsrt_decode(const qsrt_decode_job* jobs, int n_jobs, int K, const uint8_t* l
         const qsrt_decode_job& s = jobs[i];
         const bool ok = s.words && s.row_scale && s.col_scale && s.out && s.rows >= 0 && s.cols >= 0 &&
                         s.rows % 128 == 0 && s.cols % 128 == 0 && s.out_ld >= s.cols && s.out_ld % 4 == 0 &&
-                        reinterpret_cast<uintptr_t>(s.words) % 4 == 0 && s.tile_row_stride % 2 == 0 &&
-                        s.tile_col_stride % 2 == 0 && reinterpret_cast<uintptr_t>(s.out) % out_align == 0 &&
+                        reinterpret_cast<uintptr_t>(s.words) % 16 == 0 && s.tile_row_stride % 8 == 0 &&
+                        s.tile_col_stride % 8 == 0 && reinterpret_cast<uintptr_t>(s.out) % 16 == 0 &&
+                        s.out_ld % 8 == 0 &&
                         reinterpret_cast<uintptr_t>(s.col_scale) % 16 == 0;
         if (!ok) {
             free(host);
             return qsrt::fail(qsrt::kBadArgument,
-                              "decode job %d: need rows, cols multiples of 128, out_ld >= cols and % 4, 4-byte "
-                              "aligned words with even tile strides, aligned out and col_scale, non-null pointers",
+                              "decode job %d: need rows, cols multiples of 128, out_ld >= cols and a multiple of 8, "
+                              "16-byte aligned words, out and col_scale, tile strides multiples of 8, non-null pointers",
                               i);
         }
         host[i] = Job{s.words, s.tile_row_stride, s.tile_col_stride, s.row_scale, s.col_scale, s.out, s.out_ld,
@@ -286,7 +381,8 @@ int qsrt_decode(const qsrt_decode_job* jobs, int n_jobs, int K, const uint8_t* l
     if (total == 0) return qsrt::kOk;
     int cus = 0;
     if (const int rc = qsrt::current_cu_count(&cus)) return rc;
-    const unsigned grid = static_cast<unsigned>(total < cus ? total : cus);
+    const int64_t slots = 2 * static_cast<int64_t>(cus);  // two workgroups per CU
+    const unsigned grid = static_cast<unsigned>(total < slots ? total : slots);
     const Job* dj = static_cast<const Job*>(workspace);
     switch (K * 2 + (exact_fp8 ? 1 : 0)) {
         case 5: launch<2, true>(dj, n_jobs, total, lut_e4m3, out_dtype, grid, stream); break;
