@@ -36,6 +36,11 @@ CONTEXT = 128
 EDGES_PER_WEIGHT = (256 + 2 * CONTEXT) / 256 * 65536  # 131,072 at C=128
 FLOPS_PER_EDGE = 3  # d = label - x (1), fma(d, d, cost) (2)
 FP32_PEAK_TFLOPS = 157.3
+# HBM bytes per tile of the Viterbi kernel (FETCH_SIZE x 2.00 + WRITE_SIZE x 1.00 per dispatch, calibrated on a
+# 4 GiB device copy; profiles/viterbi_tiles_kernel_microbench.md): mostly the traceback decision stream.
+VITERBI_HBM_BYTES_PER_TILE = 1.629e6
+# Same counters for the decode kernel: 1.001 x its algorithmic bytes (profiles/decode_kernel_layer.md).
+DECODE_TRAFFIC_OVER_ALGORITHMIC = 1.001
 
 
 def log(msg: str) -> None:
@@ -218,6 +223,109 @@ def cpu_baseline(tiles_np, seconds_target: float = 12.0):
     }
 
 
+DECODE_MATRICES = 1152  # 384 experts x 3 matrices of the Kimi-class shape
+HBM_PEAK_GBPS = 8000.0
+
+
+def decode_bench(steps: int = 3, matrices: int = DECODE_MATRICES, bits: int = 3):
+    """Whole-layer decode (BASELINE config 5 shape): ``matrices`` packed
+    7168 x 2048 trellis payloads at rate ``bits`` -> bf16, one launch.
+    Payload words are random (any word stream is a valid cyclic path)."""
+
+    from qsrt_amd.decode import DecodePlan
+    from qsrt_amd.sqg_e4m3 import sqg_xor_cheb_t12_bytes
+
+    dev = torch.device("cuda:0")
+    k, n = 7168, 2048
+    g = torch.Generator(device=dev).manual_seed(20261201 + 5)
+    words = torch.randint(-32768, 32767, (matrices, k // 16, n // 16, 16 * bits), dtype=torch.int16, device=dev, generator=g)
+    su = (torch.rand(k, device=dev, generator=g) + 0.5) / 128.0
+    sv = torch.rand(n, device=dev, generator=g) - 0.5
+    out = torch.empty((matrices, k, n), dtype=torch.bfloat16, device=dev)
+    plan = DecodePlan([(words[i], su, sv, out[i]) for i in range(matrices)], bits, sqg_xor_cheb_t12_bytes(bits))
+    plan.run()
+    torch.cuda.synchronize()
+    ms = []
+    for _ in range(steps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        plan.run()
+        e1.record()
+        torch.cuda.synchronize()
+        ms.append(e0.elapsed_time(e1))
+    weights = matrices * k * n
+    byts = weights * (bits / 8 + 2) + matrices * (k + n) * 4
+    t = min(ms) / 1e3
+    del words, out
+    torch.cuda.empty_cache()
+    return {
+        "workload": f"{matrices} x [{k} x {n}] K{bits} payloads -> bf16 (one launch, config-5 layer shape)",
+        "kernel": "decode_kernel",
+        "ms": round(min(ms), 3),
+        "G_weights_per_s": round(weights / t / 1e9, 2),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(byts / t / 1e9, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(byts / t / 1e9 / HBM_PEAK_GBPS, 4),
+            "traffic": round(byts * DECODE_TRAFFIC_OVER_ALGORITHMIC),
+            "algorithmic": f"{bits}/8 B payload + 2 B bf16 out per weight + (K + N) f32 scales per matrix = {byts} B/launch",
+        },
+    }
+
+
+def expert_bench(bits: int = 3, cpu_seconds: float = 4.0):
+    """BASELINE config 4 at K3 (the north-star target): one warm-up and one
+    timed end-to-end encode of the coupled Kimi-class expert, and the CPU
+    oracle's per-tile time scaled by the timed run's tile-encode count (a lower
+    bound on the CPU encoder: the LDLQ products, Hessian and activation work
+    are not charged to the CPU)."""
+
+    run_expert_encode(bits=bits, log=log)
+    r = run_expert_encode(bits=bits, log=log)
+    import numpy as np
+    from oracle import tables as otables
+    from oracle import viterbi as ov
+
+    threads = ov.default_threads()
+    g = np.random.default_rng(20261201 + 4)
+    sample = g.standard_normal((max(threads, 256), 256)).astype(np.float32)
+    lab = otables.t12_values(bits)
+    ov.encode(sample[:threads], lab, K=bits, threads=threads)
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < cpu_seconds:
+        ov.encode(sample, lab, K=bits, boundary_lag=1, threads=threads)
+        n += len(sample)
+    per_tile = (time.perf_counter() - t0) / n
+    cpu_s = per_tile * r["tile_encodes"]
+    return {
+        "workload": "config 4: Kimi-class coupled expert 7168 x 2048 SwiGLU, all three matrices, K3, LDLQ, H2 from reconstructed activations",
+        "seconds": round(r["seconds"], 3),
+        "M_weights_per_s": round(r["M_weights_per_s"], 2),
+        "tile_encodes": r["tile_encodes"],
+        "phases_s": {"gate_up": round(r["seconds_upstream"], 3), "h2_rebuild": round(r["seconds_h2_rebuild"], 3),
+                     "down": round(r["seconds_down"], 3)},
+        "proxy_err": {k: round(v, 5) for k, v in r["proxy"].items()},
+        "cpu_extrapolated_seconds": round(cpu_s, 1),
+        "cpu_basis": f"oracle/viterbi_ref.c, {threads} threads, {per_tile * 1e3:.3f} ms/tile (K3, C=128) x {r['tile_encodes']} tile encodes",
+        "speedup_vs_cpu": round(cpu_s / r["seconds"], 1),
+    }
+
+
+def copy_calibration(nbytes: int) -> None:
+    """A plain device copy of ``nbytes`` (the known-size reference for the
+    HBM byte counters)."""
+
+    x = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda:0").fill_(1.0)
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    y.copy_(x)
+    torch.cuda.synchronize()
+    log(f"[bench] copied {nbytes} bytes")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -225,14 +333,21 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--tiles", type=int, default=TILES)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-expert", action="store_true", help="skip the config-4 expert encode")
+    ap.add_argument("--no-decode", action="store_true", help="skip the layer decode")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run a device copy of BYTES (reference for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the encoder hot path is a single-GPU kernel here; "
               "multi-GPU sharding is design-only (see DESIGN.md)", file=sys.stderr)
         return 2
 
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return 0
+
     import numpy as np
-    import torch
 
     from qsrt_amd.sqg_e4m3 import sqg_xor_cheb_t12_bytes
     from qsrt_amd.sqg_quantizer import boundary_lag, viterbi_tiles
@@ -308,7 +423,7 @@ def main() -> int:
             "peak": FP32_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": round(VITERBI_HBM_BYTES_PER_TILE * args.tiles),
             "kernel": "viterbi_tiles_kernel",
             "algorithmic": f"{FLOPS_PER_EDGE} FP32 flops/edge x {int(EDGES_PER_WEIGHT)} edges/weight x {weights_per_k} weights/launch",
         },
@@ -317,6 +432,16 @@ def main() -> int:
         log("[bench] CPU baseline (oracle) on a bounded sample")
         result["cpu_baseline"] = cpu_baseline(tiles_cpu.numpy())
         result["cpu_baseline"]["gpu_speedup"] = round(value / result["cpu_baseline"]["value"], 1)
+    del tiles, outs
+    torch.cuda.empty_cache()
+    if not args.no_decode:
+        log("[bench] layer decode")
+        result["decode"] = decode_bench()
+        log(f"[bench] decode {result['decode']['roofline']['achieved']} GB/s")
+    if not args.no_expert:
+        log("[bench] config-4 expert encode (K3)")
+        result["expert_encode"] = expert_bench()
+        log(f"[bench] expert {result['expert_encode']['seconds']} s, {result['expert_encode']['speedup_vs_cpu']}x CPU")
     print(json.dumps(result), flush=True)
     return 0
 

@@ -122,3 +122,40 @@ def decode_packed(packed, suh: torch.Tensor, svh: torch.Tensor, luts_by_bits: di
     for bits, jobs in sorted(by_bits.items()):
         _run(jobs, bits, _check_lut(luts_by_bits[bits], dev), out_dtype, dev)
     return out
+
+
+class DecodePlan:
+    """A fixed set of uniform-rate matrices decoded by one launch.
+
+    ``matrices`` is a list of ``(words [K/16, N/16, 16 bits], su f32 [K] (already
+    divided by 128), sv f32 [N], out [K, N])`` on one device; the job table is
+    built once, so ``run()`` only uploads it and launches."""
+
+    def __init__(self, matrices: list, bits: int, lut: torch.Tensor, *, out_dtype=torch.bfloat16):
+        if not matrices:
+            raise ValueError("empty decode plan")
+        dev = matrices[0][0].device
+        self.bits, self.device, self.out_dtype = bits, dev, out_dtype
+        self.lut = _check_lut(lut, dev)
+        self._keep = matrices
+        jobs = []
+        for words, su, sv, out in matrices:
+            kt, nt, wpt = words.shape
+            if wpt != 16 * bits or out.shape != (16 * kt, 16 * nt) or out.dtype != out_dtype:
+                raise ValueError("decode plan entry does not match its output")
+            jobs.append(_native.DecodeJob(words.data_ptr(), nt * 16 * bits, 16 * bits, su.data_ptr(), sv.data_ptr(),
+                                          out.data_ptr(), out.stride(0), 16 * kt, 16 * nt))
+        self._arr = (_native.DecodeJob * len(jobs))(*jobs)
+        self._n = len(jobs)
+        lib = _native.lib()
+        self._ws = torch.empty(max(int(lib.qsrt_decode_workspace_bytes(self._n)), 16), dtype=torch.uint8, device=dev)
+        self._fp8 = int(_lut_abs_max(self.lut) <= FP8_EXACT_MAX_LABEL)
+
+    def run(self) -> None:
+        lib = _native.lib()
+        _native.check(
+            lib.qsrt_decode(ctypes.cast(self._arr, ctypes.c_void_p), self._n, self.bits, self.lut.data_ptr(),
+                            self._fp8, _OUT[self.out_dtype], self._ws.data_ptr(), self._ws.numel(),
+                            _native.stream_handle(self.device)),
+            "qsrt_decode",
+        )
