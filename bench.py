@@ -77,53 +77,21 @@ def ar1_rows(n: int, k: int, rho: float, gen: torch.Generator, device) -> torch.
     return (z.double() @ T).float()
 
 
-def block_wht(x: torch.Tensor, block: int, dim: int) -> torch.Tensor:
-    """Normalised Sylvester Hadamard over ``block``-sized groups of ``dim``."""
-
-    from qsrt_amd.exl3_reference import normalized_hadamard
-
-    h = normalized_hadamard(device=x.device, dtype=torch.float32, size=block)
-    x = x.float().movedim(dim, -1)
-    shape = x.shape
-    y = (x.reshape(*shape[:-1], shape[-1] // block, block) @ h).reshape(shape)
-    return y.movedim(-1, dim).contiguous()
-
-
-def coupled_expert(w_gate, w_up, w_down):
-    """Exact coupled basis with the zero draw (all-ones signs): interleave
-    gate/up rows, Hadamard 512 along hidden and 128 along the interleaved
-    rows; down gets 128 along intermediate and 512 along hidden
-    (reference qsrt/qsrt_coupled.py:145-196)."""
-
-    inter = w_gate.shape[0]
-    inter2 = torch.stack((w_gate, w_up), dim=1).reshape(2 * inter, -1)
-    up = block_wht(block_wht(inter2, 512, 1), 128, 0)
-    down = block_wht(block_wht(w_down, 128, 1), 512, 0)
-    return up[:inter].contiguous(), up[inter:].contiguous(), down
-
-
-def uncoupled_upstream(g_c, u_c):
-    """Inverse of the upstream part of :func:`coupled_expert` (self-inverse
-    Hadamards, then de-interleave)."""
-
-    inter = g_c.shape[0]
-    x = torch.cat((g_c, u_c), dim=0)
-    x = block_wht(block_wht(x, 128, 0), 512, 1)
-    x = x.reshape(inter, 2, -1)
-    return x[:, 0].contiguous(), x[:, 1].contiguous()
-
-
 def run_expert_encode(bits: int = 3, hidden: int = 7168, inter: int = 2048, tokens: int = 16384, rho: float = 0.85, log=print):
     """BASELINE config 4 at rate ``bits``: one Kimi-class SwiGLU expert in the
-    exact coupled basis, H13 from ``tokens`` AR(1) rows, H2 rebuilt from the
-    reconstructed gate/up SwiGLU activations, all three matrices encoded with
-    BlockLDLQ.  Returns timing and quality figures."""
+    exact coupled basis (qsrt_amd.qsrt_coupled, draw 0), H13 = X^T X from
+    ``tokens`` AR(1) rows (captured before the timed region, as the reference
+    receives it), H2 rebuilt inside the timed region from the reconstructed
+    gate/up SwiGLU activations, all three matrices encoded with BlockLDLQ.
+    Returns timing and quality figures."""
 
     from qsrt_amd import exl3_encoder_backend as be
-    from qsrt_amd import qsrt as Q
-    from qsrt_amd.exl3_reference import decode_exl3_weight
+    from qsrt_amd.decode import decode_words
     from qsrt_amd.ldlq import make_shared_h
     from qsrt_amd.sqg_e4m3 import sqg_xor_cheb_t12_bytes
+
+    from qsrt_amd import gemm
+    from qsrt_amd.qsrt_coupled import CoupledHadamardSpec, coupled_execution, decode_coupled_weights, encode_coupled_weights
 
     dev = torch.device("cuda:0")
     gen = torch.Generator().manual_seed(20261201 + 4)
@@ -132,8 +100,11 @@ def run_expert_encode(bits: int = 3, hidden: int = 7168, inter: int = 2048, toke
     w_down = student_t((hidden, inter), nu=5, std=0.015, gen=gen).bfloat16().float().to(dev)
     x = ar1_rows(tokens, hidden, rho, gen, dev)
     torch.cuda.synchronize()
-    g_c, u_c, d_c = coupled_expert(w_gate, w_up, w_down)
-    h13 = block_wht(block_wht(x.T @ x, 512, 0), 512, 1)  # transform_h13 with unit signs
+    spec = CoupledHadamardSpec()  # residual 512, pre/post 128, draw 0
+    g_c, u_c, d_c = encode_coupled_weights((w_gate, w_up, w_down), spec)
+    ex = coupled_execution((g_c, u_c, d_c), spec)
+    h13 = gemm.gram_(torch.zeros((hidden, hidden), device=dev), x)  # H13 = X^T X on the FP32 matrix cores
+    h13 = ex.transform_h13(h13)
     lut = sqg_xor_cheb_t12_bytes(bits)
     tiles_encoded = [0]
     real = be.quantize_tiles_multigpu
@@ -156,11 +127,11 @@ def run_expert_encode(bits: int = 3, hidden: int = 7168, inter: int = 2048, toke
         (pg, tg), (pu, tu) = be.quantize_uniform_batch([g_c.T.contiguous(), u_c.T.contiguous()], [shared13, shared13], [qa_g, qa_u])
         torch.cuda.synchronize()
         t_upstream = time.perf_counter() - t0
-        # H2 from the reconstructed gate/up activations in the source basis
-        dec = lambda t: decode_exl3_weight(Q.unpack_trellis_states(t["trellis"], bits), t["suh"], t["svh"], bits=bits).T
-        g_hat, u_hat = uncoupled_upstream(dec(tg), dec(tu))
-        h = torch.nn.functional.silu(x @ g_hat.T) * (x @ u_hat.T)
-        h2 = block_wht(block_wht(h.T @ h, 128, 0), 128, 1)  # transform_h2 with unit signs
+        # H2 from the reconstructed gate/up SwiGLU activations (source basis), then the coupled transform
+        dec = lambda t: decode_words(t["trellis"], t["suh"], t["svh"], bits, lut, out_dtype=torch.float32).T
+        g_hat, u_hat, _ = decode_coupled_weights((dec(tg), dec(tu), d_c), spec)
+        h = (torch.nn.functional.silu(x @ g_hat.T) * (x @ u_hat.T)).contiguous()
+        h2 = ex.transform_h2(gemm.gram_(torch.zeros((inter, inter), device=dev), h))
         del h
         shared2 = make_shared_h(inter, dev, h2)
         shared2["count"] = tokens

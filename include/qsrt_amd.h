@@ -133,6 +133,19 @@ size_t qsrt_decode_workspace_bytes(int n_jobs);
 int qsrt_decode(const qsrt_decode_job *jobs, int n_jobs, int K, const uint8_t *lut_e4m3, int exact_fp8,
                 int out_dtype, void *workspace, size_t workspace_bytes, void *stream);
 
+/*
+ * C[M, N] += alpha * A^T (B - B2) on the matrix cores, all row-major:
+ *   A [K, M] (lda), B and B2 [K, N] (ldb), C [M, N] f32 (ldc).
+ *   dtype 0: f32 operands (16-byte aligned, lda/ldb multiples of 4), exact
+ *            FP32 products; B2 may be NULL (no subtraction).
+ *   dtype 1: bf16 operands (raw uint16 bits), FP32 accumulation; B2 NULL.
+ * Replaces the BlockLDLQ feedback products prod_cache += L^T (W - Q)
+ * (qsrt/exl3_encoder_backend.py:496, :534; batched :1170-1187) and the
+ * Hessian capture H += X^T X.
+ */
+int qsrt_gemm_tn(float *C, const void *A, const void *B, const void *B2, int64_t M, int64_t N, int64_t K,
+                 int64_t lda, int64_t ldb, int64_t ldc, float alpha, int dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -39,6 +39,11 @@ SIGNATURES: dict[str, tuple] = {
     "qsrt_unpack_states": (_c_int, [_c_void_p, _c_i64, _c_int, _c_void_p, _c_void_p]),
     "qsrt_decode_workspace_bytes": (_c_size, [_c_int]),
     "qsrt_decode": (_c_int, [_c_void_p, _c_int, _c_int, _c_void_p, _c_int, _c_int, _c_void_p, _c_size, _c_void_p]),
+    "qsrt_gemm_tn": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float,
+         _c_int, _c_void_p],
+    ),
     "qsrt_hadamard": (
         _c_int,
         [_c_void_p, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p],

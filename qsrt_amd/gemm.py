@@ -1,25 +1,104 @@
 """Dense products of the BlockLDLQ recursion and of Hessian capture.
 
-``addmm_tn_(C, A, B)``: ``C += A^T @ B`` in FP32 (the LDLQ feedback
-products, reference ``exl3_encoder_backend.py:496``, ``:534``).
-``baddbmm_tn_``: the same per batch member.
+Device tensors run the HIP matrix-core kernel behind ``qsrt_gemm_tn``
+(``include/qsrt_amd.h``): FP32 operands with exact products and FP32
+accumulation for the feedback ``C += A^T (B - B2)`` (reference
+``exl3_encoder_backend.py:496``, ``:534``, batched ``:1170-1187``), bf16
+operands for ``H += X^T X``.  CPU tensors use torch in FP32.
 """
 
 from __future__ import annotations
 
 import torch
 
+from . import _native
 
-def _fp32_matmul_policy():
-    # IEEE FP32 products: TF32 would change the feedback targets.
-    torch.backends.cuda.matmul.allow_tf32 = False
+
+def _row_major(t: torch.Tensor) -> bool:
+    return t.dim() == 2 and t.stride(1) == 1 and t.stride(0) >= t.shape[1]
+
+
+def _launch(C, A, B, B2, alpha, dtype):
+    K, M = A.shape
+    N = B.shape[1]
+    lib = _native.lib()
+    _native.check(
+        lib.qsrt_gemm_tn(C.data_ptr(), A.data_ptr(), B.data_ptr(), None if B2 is None else B2.data_ptr(), M, N, K,
+                         A.stride(0), B.stride(0), C.stride(0), float(alpha), dtype, _native.stream_handle(C.device)),
+        "qsrt_gemm_tn",
+    )
+
+
+def _copy_padded(t: torch.Tensor, ld: int) -> torch.Tensor:
+    rows, cols = t.shape
+    view = torch.empty((rows, ld), dtype=t.dtype, device=t.device)[:, :cols]
+    view.copy_(t)
+    return view
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """``t`` as a row-major matrix with a 16-byte aligned base and a leading
+    dimension that is a multiple of 4 elements (copied into a padded buffer
+    when needed)."""
+
+    if _row_major(t) and t.data_ptr() % 16 == 0 and t.stride(0) % 4 == 0:
+        return t
+    return _copy_padded(t, (t.shape[1] + 3) // 4 * 4)
+
+
+def addmm_sub_tn_(C: torch.Tensor, A: torch.Tensor, B: torch.Tensor, B2: torch.Tensor | None = None,
+                  alpha: float = 1.0) -> torch.Tensor:
+    """``C += alpha * A^T (B - B2)`` in place (``B2`` optional)."""
+
+    K, M = A.shape
+    if B.shape[0] != K or C.shape != (M, B.shape[1]) or (B2 is not None and B2.shape != B.shape):
+        raise ValueError("addmm_sub_tn_: incompatible shapes")
+    if C.is_cuda:
+        if C.dtype != torch.float32 or A.dtype != torch.float32 or B.dtype != torch.float32:
+            raise ValueError("addmm_sub_tn_: float32 operands expected")
+        A, B = _aligned(A), _aligned(B)
+        if B2 is not None:
+            B2 = _aligned(B2)
+            if B2.stride(0) != B.stride(0):  # one leading dimension serves both
+                ld = (B.shape[1] + 3) // 4 * 4
+                B, B2 = _copy_padded(B, ld), _copy_padded(B2, ld)
+        if not _row_major(C):
+            raise ValueError("addmm_sub_tn_: C must be row-major")
+        _launch(C, A, B, B2, alpha, 0)
+        return C
+    rhs = B if B2 is None else B - B2
+    return C.addmm_(A.T, rhs, alpha=alpha)
 
 
 def addmm_tn_(C: torch.Tensor, A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
-    _fp32_matmul_policy()
-    return C.addmm_(A.T, B)
+    """``C += A^T @ B`` in FP32."""
+
+    return addmm_sub_tn_(C, A, B)
 
 
 def baddbmm_tn_(C: torch.Tensor, A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
-    _fp32_matmul_policy()
-    return C.baddbmm_(A.transpose(1, 2), B)
+    """Per batch member ``C[b] += A[b]^T @ B[b]``."""
+
+    for b in range(C.shape[0]):
+        addmm_sub_tn_(C[b], A[b], B[b])
+    return C
+
+
+def gram_(H: torch.Tensor, X: torch.Tensor, alpha: float = 1.0) -> torch.Tensor:
+    """``H += alpha * X^T X`` (Hessian capture); bf16 ``X`` on the bf16 matrix
+    cores, float32 ``X`` on the FP32 path."""
+
+    n, k = X.shape
+    if H.shape != (k, k) or H.dtype != torch.float32:
+        raise ValueError("gram_: H must be float32 [k, k]")
+    if H.is_cuda:
+        X = X.contiguous()
+        if X.dtype == torch.bfloat16:
+            _launch(H, X, X, None, alpha, 1)
+        elif X.dtype == torch.float32:
+            _launch(H, X, X, None, alpha, 0)
+        else:
+            raise ValueError("gram_: X must be bfloat16 or float32")
+        return H
+    Xf = X.float()
+    return H.addmm_(Xf.T, Xf, alpha=alpha)

@@ -1,0 +1,76 @@
+"""HIP matrix-core GEMM (qsrt_gemm_tn) against float64: the fused BlockLDLQ
+feedback product C += alpha A^T (B - B2) in FP32 and the bf16 Hessian
+capture H += X^T X, at ragged shapes, strided views and the LDLQ shapes."""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from qsrt_amd import gemm
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel(got, want):
+    return float(np.max(np.abs(got - want)) / max(np.abs(want).max(), 1e-30))
+
+
+@pytest.mark.parametrize("M,N,K", [(16, 256, 112), (200, 300, 77), (128, 128, 16), (1, 5, 3), (640, 4096, 128)])
+def test_fused_feedback_product_matches_float64(M, N, K):
+    print(f"[gemm] f32 M{M} N{N} K{K}", file=sys.stderr, flush=True)
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    A = torch.randn(K, M, generator=g)
+    B = torch.randn(K, N, generator=g)
+    B2 = torch.randn(K, N, generator=g)
+    C = torch.randn(M, N, generator=g)
+    want = C.double().numpy() + 0.5 * (A.double().numpy().T @ (B.double().numpy() - B2.double().numpy()))
+    Cg = C.cuda()
+    gemm.addmm_sub_tn_(Cg, A.cuda(), B.cuda(), B2.cuda(), alpha=0.5)
+    assert _rel(Cg.cpu().double().numpy(), want) < 1e-5
+    Cg = C.cuda()
+    gemm.addmm_tn_(Cg, A.cuda(), B.cuda())
+    assert _rel(Cg.cpu().double().numpy(), C.double().numpy() + A.double().numpy().T @ B.double().numpy()) < 1e-5
+
+
+def test_strided_ldlq_views():
+    # L[begin:end, :begin]^T (W - Q)[begin:end] into prod_cache[:begin], the span update of the recursion
+    g = torch.Generator().manual_seed(3)
+    k, n, begin, end = 512, 384, 256, 384
+    L = torch.randn(k, k, generator=g).cuda()
+    W = torch.randn(k, n, generator=g).cuda()
+    Q = torch.randn(k, n, generator=g).cuda()
+    P = torch.zeros(k, n).cuda()
+    gemm.addmm_sub_tn_(P[:begin], L[begin:end, :begin], W[begin:end], Q[begin:end])
+    want = L[begin:end, :begin].double().cpu().numpy().T @ (W[begin:end] - Q[begin:end]).double().cpu().numpy()
+    assert _rel(P[:begin].cpu().double().numpy(), want) < 1e-5
+    assert bool((P[begin:] == 0).all())
+    # the per-block product with a 16-column slice of L (unaligned to the 128 tile)
+    blk, blk_end = 272, 288
+    comp = torch.zeros(16, n).cuda()
+    gemm.addmm_sub_tn_(comp, L[blk_end:end, blk:blk_end], W[blk_end:end], Q[blk_end:end])
+    want = L[blk_end:end, blk:blk_end].double().cpu().numpy().T @ (W[blk_end:end] - Q[blk_end:end]).double().cpu().numpy()
+    assert _rel(comp.cpu().double().numpy(), want) < 1e-5
+
+
+@pytest.mark.parametrize("n,k", [(4096, 256), (1000, 200)])
+def test_bf16_gram_matches_float64(n, k):
+    print(f"[gemm] bf16 gram n{n} k{k}", file=sys.stderr, flush=True)
+    g = torch.Generator().manual_seed(n + k)
+    X = torch.randn(n, k, generator=g).bfloat16()
+    H = torch.zeros(k, k).cuda()
+    gemm.gram_(H, X.cuda(), alpha=1.0 / n)
+    x64 = X.double().numpy()
+    assert _rel(H.cpu().double().numpy(), x64.T @ x64 / n) < 1e-5
+    Hf = torch.zeros(k, k).cuda()
+    gemm.gram_(Hf, X.float().cuda())
+    assert _rel(Hf.cpu().double().numpy(), x64.T @ x64) < 1e-5
+
+
+def test_gemm_rejects_bad_arguments():
+    A = torch.randn(4, 4).cuda()
+    with pytest.raises(ValueError):
+        gemm.addmm_sub_tn_(torch.zeros(4, 5).cuda(), A, torch.randn(4, 4).cuda())
