@@ -74,6 +74,37 @@ RECORDS_PER_EXPERT = KIMI_K3.records
 PAIRS_PER_EXPERT = RECORDS_PER_EXPERT // 2
 FIXED_HIGH_RATE_RECORD_BITS = (3,) * 22 + (4,) * 2
 
+# Layer-level format constants (reference qsrt.py:33-90).
+EXPERTS_PER_LAYER = 896
+MOE_LAYERS = range(1, 93)
+CONTEXT_GROUP_CHANNELS = 4
+PAIR_CHANNELS = 2 * RECORD_CHANNELS
+PAIR_ROTATION_EXPERT_MULTIPLIER = 5
+FORMAT_BITS = 8
+FORMAT_X4T = 0xFF
+FORMAT_NIBBLE_MASK = 0x0F
+LAYER_HEADER_BYTES = STORAGE_ALIGNMENT
+FORMAT_TABLE_BYTES = (EXPERTS_PER_LAYER * FORMAT_BITS + 7) // 8
+FORMAT_SECTION_BYTES = STORAGE_ALIGNMENT
+HOT_FORMAT_BYTES = EXPERTS_PER_LAYER
+HOT_SLOT_BYTES = EXPERTS_PER_LAYER * 2
+HOT_METADATA_BYTES = HOT_FORMAT_BYTES + HOT_SLOT_BYTES
+SHARED_SCALE_VECTORS = 3
+LOCAL_SCALE_VECTORS = 3
+SHARED_SCALE_ORDER = ("w1.suh", "w3.suh", "w2.svh")
+LOCAL_SCALE_ORDER = ("w1.svh", "w3.svh", "w2.suh")
+SCALE_BYTES = 2
+SHARED_SCALE_BYTES = SHARED_SCALE_VECTORS * LATENT_CHANNELS * SCALE_BYTES
+SHARED_SCALE_SECTION_BYTES = 6 * STORAGE_ALIGNMENT
+PAIR_BYTES = PAIR_CHANNELS * LATENT_CHANNELS * 3 // 8
+MATRIX_TRELLIS_BYTES = PAIRS_PER_EXPERT * PAIR_BYTES
+EXPERT_TRELLIS_BYTES = 3 * MATRIX_TRELLIS_BYTES
+FIXED_HIGH_RATE_TRELLIS_BYTES = (
+    INTERMEDIATE_CHANNELS * LATENT_CHANNELS * sum(FIXED_HIGH_RATE_RECORD_BITS) // (RECORDS_PER_EXPERT * 8)
+)
+PURE_K2_MATRIX_TRELLIS_BYTES = INTERMEDIATE_CHANNELS * LATENT_CHANNELS * 2 // 8
+PURE_K2_EXPERT_TRELLIS_BYTES = 3 * PURE_K2_MATRIX_TRELLIS_BYTES
+
 
 # ---------------------------------------------------------------------------
 # Rate modes (reference qsrt.py:143-236, :516-561)
@@ -575,3 +606,386 @@ def mode_from_context_bits(context_bits: Sequence[int], geometry: Geometry = KIM
     r = bits.count(2) * (geometry.records // len(bits))
     ModeSpec(r, "candidate", bits, geometry)
     return rate_transfer_mode(r, geometry)
+
+
+# ---------------------------------------------------------------------------
+# Physical pair placement (reference qsrt.py:101-141)
+# ---------------------------------------------------------------------------
+
+
+def _check_int(value, lo: int, hi: int, message: str) -> int:
+    if isinstance(value, bool) or not isinstance(value, int) or not lo <= value < hi:
+        raise ValueError(message)
+    return value
+
+
+def pair_rotation(layer: int, expert: int, geometry: Geometry = KIMI_K3) -> int:
+    """Cyclic logical-pair placement balancing physical atom slots:
+    ``(5 expert + layer) mod pairs``."""
+
+    _check_int(layer, 1, 93, "K3 MoE layer must be in 1..92")
+    _check_int(expert, 0, EXPERTS_PER_LAYER, f"expert must be in 0..{EXPERTS_PER_LAYER - 1}")
+    return (PAIR_ROTATION_EXPERT_MULTIPLIER * expert + layer) % (geometry.records // 2)
+
+
+def logical_pair_for_slot(layer: int, expert: int, pair_slot: int, geometry: Geometry = KIMI_K3) -> int:
+    pairs = geometry.records // 2
+    _check_int(pair_slot, 0, pairs, f"pair_slot must be in 0..{pairs - 1}")
+    return (pair_slot - pair_rotation(layer, expert, geometry)) % pairs
+
+
+def physical_pair_slot(layer: int, expert: int, logical_pair: int, geometry: Geometry = KIMI_K3) -> int:
+    pairs = geometry.records // 2
+    _check_int(logical_pair, 0, pairs, f"logical_pair must be in 0..{pairs - 1}")
+    return (logical_pair + pair_rotation(layer, expert, geometry)) % pairs
+
+
+# ---------------------------------------------------------------------------
+# Per-expert format codes and layer metadata sections (reference :257-491)
+# ---------------------------------------------------------------------------
+
+
+@dataclass(frozen=True)
+class ExpertFormatSpec:
+    """Per-expert tier: ``None/None`` is the exact X4T tier, else the w1/w3
+    (``r13``) and w2 (``r2``) mode IDs packed as one byte ``r13 << 4 | r2``."""
+
+    r13: int | None
+    r2: int | None
+
+    def __post_init__(self) -> None:
+        if (self.r13 is None) != (self.r2 is None):
+            raise ValueError("r13 and r2 must both be absent or both be present")
+        for name, value in (("r13", self.r13), ("r2", self.r2)):
+            if value is None:
+                continue
+            if isinstance(value, bool) or not isinstance(value, int):
+                raise TypeError(f"{name} must be an integer")
+            if not 0 <= value <= 4:
+                raise ValueError(f"{name} must identify R0, R1, R2, H308, or K2")
+        if self.r13 is not None:
+            fixed = {H308.mode_id, K2.mode_id}
+            if (self.r13 in fixed or self.r2 in fixed) and self.r13 != self.r2:
+                raise ValueError("H308 and K2 must be selected for both matrix rate axes")
+
+    @classmethod
+    def x4t(cls) -> "ExpertFormatSpec":
+        return cls(None, None)
+
+    @classmethod
+    def compressed(cls, r13: int, r2: int | None = None) -> "ExpertFormatSpec":
+        return cls(r13, r13 if r2 is None else r2)
+
+    @property
+    def is_x4t(self) -> bool:
+        return self.r13 is None
+
+    @property
+    def name(self) -> str:
+        if self.is_x4t:
+            return "X4T"
+        if self.r13 == self.r2 == H308.mode_id:
+            return H308.name
+        if self.r13 == self.r2 == K2.mode_id:
+            return K2.name
+        return f"R{self.r13}" if self.r13 == self.r2 else f"R{self.r13}/R{self.r2}"
+
+    @property
+    def code(self) -> int:
+        return FORMAT_X4T if self.is_x4t else (self.r13 << 4) | self.r2
+
+    @classmethod
+    def from_code(cls, code: int) -> "ExpertFormatSpec":
+        if code == FORMAT_X4T:
+            return cls.x4t()
+        r13, r2 = code >> 4, code & FORMAT_NIBBLE_MASK
+        if r13 > 4 or r2 > 4:
+            raise ValueError(f"format table contains invalid rate code 0x{code:02x}")
+        return cls.compressed(r13, r2)
+
+
+def resolve_expert_format(value) -> ExpertFormatSpec:
+    if isinstance(value, ExpertFormatSpec):
+        return value
+    if isinstance(value, ModeSpec):
+        return ExpertFormatSpec.compressed(value.mode_id)
+    if isinstance(value, tuple):
+        if len(value) != 2:
+            raise ValueError("expert format tuple must be (r13, r2)")
+        return ExpertFormatSpec.compressed(value[0], value[1])
+    if not isinstance(value, str):
+        raise TypeError("expert format must be a name, ModeSpec, ExpertFormatSpec, or pair")
+    name = value.upper()
+    if name == "X4T":
+        return ExpertFormatSpec.x4t()
+    if "/" in name:
+        left, right = name.split("/", 1)
+        return ExpertFormatSpec.compressed(resolve_mode(left).mode_id, resolve_mode(right).mode_id)
+    return ExpertFormatSpec.compressed(resolve_mode(name).mode_id)
+
+
+def pack_qsrt_format_table(formats: Sequence) -> torch.Tensor:
+    """One byte per expert of the layer."""
+
+    if len(formats) != EXPERTS_PER_LAYER:
+        raise ValueError(f"format table must contain {EXPERTS_PER_LAYER} experts")
+    return torch.tensor([resolve_expert_format(v).code for v in formats], dtype=torch.uint8)
+
+
+def unpack_qsrt_format_table(payload: torch.Tensor) -> tuple[str, ...]:
+    if payload.dtype != torch.uint8:
+        raise TypeError("format table must use torch.uint8")
+    if payload.ndim != 1 or payload.numel() != FORMAT_TABLE_BYTES:
+        raise ValueError(f"format table must contain exactly {FORMAT_TABLE_BYTES} bytes")
+    return tuple(ExpertFormatSpec.from_code(code).name for code in payload.cpu().tolist())
+
+
+def pack_qsrt_format_section(formats: Sequence) -> torch.Tensor:
+    """The 4 KiB on-disk format section: the table, zero padded."""
+
+    section = torch.zeros(FORMAT_SECTION_BYTES, dtype=torch.uint8)
+    section[:FORMAT_TABLE_BYTES].copy_(pack_qsrt_format_table(formats))
+    return section
+
+
+def unpack_qsrt_format_section(payload: torch.Tensor) -> tuple[str, ...]:
+    if payload.dtype != torch.uint8:
+        raise TypeError("format section must use torch.uint8")
+    if payload.ndim != 1 or payload.numel() != FORMAT_SECTION_BYTES:
+        raise ValueError(f"format section must contain exactly {FORMAT_SECTION_BYTES} bytes")
+    if bool(torch.any(payload[FORMAT_TABLE_BYTES:] != 0)):
+        raise ValueError("format section has nonzero alignment padding")
+    return unpack_qsrt_format_table(payload[:FORMAT_TABLE_BYTES])
+
+
+def expand_qsrt_hot_metadata(formats: Sequence) -> tuple[torch.Tensor, torch.Tensor]:
+    """Format codes and int16 tier-local slots (X4T and compressed experts
+    are numbered separately, in expert order)."""
+
+    codes = pack_qsrt_format_table(formats)
+    unpack_qsrt_format_table(codes)
+    slots = torch.empty(EXPERTS_PER_LAYER, dtype=torch.int16)
+    kept = compressed = 0
+    for expert, code in enumerate(codes.tolist()):
+        if code == FORMAT_X4T:
+            slots[expert] = kept
+            kept += 1
+        else:
+            slots[expert] = compressed
+            compressed += 1
+    return codes, slots
+
+
+def pack_qsrt_shared_scale_section(w1_suh: torch.Tensor, w3_suh: torch.Tensor, w2_svh: torch.Tensor,
+                                   geometry: Geometry = KIMI_K3) -> torch.Tensor:
+    """The three layer-shared hidden-side FP16 vectors, zero padded to six
+    4 KiB pages."""
+
+    scales = (w1_suh, w3_suh, w2_svh)
+    device = scales[0].device
+    for name, scale in zip(SHARED_SCALE_ORDER, scales, strict=True):
+        _validate_scale_vector(scale, geometry.latent_channels, name, device)
+    shared = SHARED_SCALE_VECTORS * geometry.latent_channels * SCALE_BYTES
+    section = torch.zeros(align_up(shared) if geometry != KIMI_K3 else SHARED_SCALE_SECTION_BYTES,
+                          dtype=torch.uint8, device=device)
+    cursor = 0
+    for scale in scales:
+        raw = scale.view(torch.uint8)
+        section[cursor:cursor + raw.numel()].copy_(raw)
+        cursor += raw.numel()
+    return section
+
+
+def unpack_qsrt_shared_scale_section(payload: torch.Tensor, geometry: Geometry = KIMI_K3):
+    shared = SHARED_SCALE_VECTORS * geometry.latent_channels * SCALE_BYTES
+    size = align_up(shared) if geometry != KIMI_K3 else SHARED_SCALE_SECTION_BYTES
+    if payload.dtype != torch.uint8:
+        raise TypeError("shared scale section must use torch.uint8")
+    if payload.ndim != 1 or payload.numel() != size:
+        raise ValueError(f"shared scale section must contain exactly {size} bytes")
+    if bool(torch.any(payload[shared:] != 0)):
+        raise ValueError("shared scale section has nonzero alignment padding")
+    out, cursor, nbytes = [], 0, geometry.latent_channels * SCALE_BYTES
+    for name in SHARED_SCALE_ORDER:
+        vector = payload[cursor:cursor + nbytes].clone().view(torch.float16).contiguous()
+        _validate_scale_vector(vector, geometry.latent_channels, name)
+        out.append(vector)
+        cursor += nbytes
+    return tuple(out)
+
+
+# ---------------------------------------------------------------------------
+# Context groups, record orders and channel permutations (reference :564-853)
+# ---------------------------------------------------------------------------
+
+
+def _validate_block_contexts(block_contexts: torch.Tensor, mode: ModeSpec) -> None:
+    groups = mode.geometry.intermediate_channels // CONTEXT_GROUP_CHANNELS
+    if block_contexts.ndim != 1 or block_contexts.numel() != groups:
+        raise ValueError(f"block_contexts must contain {groups} four-channel groups")
+    if block_contexts.dtype == torch.bool or block_contexts.is_floating_point():
+        raise TypeError("block_contexts must use an integer dtype")
+    if int(block_contexts.min()) < 0 or int(block_contexts.max()) >= mode.context_count:
+        raise ValueError("block_contexts contains an out-of-range context ID")
+    counts = torch.bincount(block_contexts.to(torch.long), minlength=mode.context_count)
+    if counts.tolist() != [groups // mode.context_count] * mode.context_count:
+        raise ValueError("every context must have equal population")
+
+
+def importance_group_order(block_contexts: torch.Tensor, mode) -> torch.Tensor:
+    """Stable low-to-high context order of the four-channel groups (the LDLQ
+    traversal order)."""
+
+    spec = resolve_mode(mode)
+    _validate_block_contexts(block_contexts, spec)
+    return torch.argsort(block_contexts, stable=True)
+
+
+def storage_group_order(block_contexts: torch.Tensor, mode) -> torch.Tensor:
+    """Physical group order: records of context ``c`` interleaved with
+    records of ``count - 1 - c`` so consecutive records form P24/P33 pairs."""
+
+    spec = resolve_mode(mode)
+    _validate_block_contexts(block_contexts, spec)
+    if spec.mode_id in (H308.mode_id, K2.mode_id):
+        return torch.argsort(block_contexts, stable=True)
+    per_record = spec.geometry.record_channels // CONTEXT_GROUP_CHANNELS
+    by_context = [torch.nonzero(block_contexts == ctx).flatten().reshape(-1, per_record)
+                  for ctx in range(spec.context_count)]
+    chunks = []
+    for low in range(spec.context_count // 2):
+        lo, hi = by_context[low], by_context[spec.context_count - 1 - low]
+        if lo.shape != hi.shape:
+            raise ValueError("paired contexts have different record populations")
+        for record in range(lo.shape[0]):
+            chunks.extend((lo[record], hi[record]))
+    return torch.cat(chunks)
+
+
+def rate_transfer_record_order(donor_records: Sequence[int], recipient_records: Sequence[int], *,
+                               middle_records: Sequence[int] | None = None,
+                               geometry: Geometry = KIMI_K3) -> tuple[int, ...]:
+    """Low-to-high record order for an equal-rate exchange: donors first
+    (K2 end), recipients reversed last (K4 end), so donor ``i`` and recipient
+    ``i`` land in one physical P24 pair."""
+
+    donors, recipients = tuple(donor_records), tuple(recipient_records)
+    records = geometry.records
+    if len(donors) != len(recipients):
+        raise ValueError("donor and recipient record counts must match")
+    if len(donors) > records // 2:
+        raise ValueError(f"at most {records // 2} rate exchanges are allowed")
+    selected = donors + recipients
+    if any(isinstance(r, bool) or not isinstance(r, int) or not 0 <= r < records for r in selected):
+        raise ValueError(f"record IDs must be integers in 0..{records - 1}")
+    if len(set(selected)) != len(selected):
+        raise ValueError("donor and recipient records must be unique and disjoint")
+    remaining = tuple(r for r in range(records) if r not in set(selected))
+    if middle_records is None:
+        middle = remaining
+    else:
+        middle = tuple(middle_records)
+        if len(middle) != len(remaining) or set(middle) != set(remaining):
+            raise ValueError("middle_records must be a permutation of all unselected records")
+    return donors + middle + tuple(reversed(recipients))
+
+
+def relabel_block_contexts_for_record_order(block_contexts: torch.Tensor, record_order: Sequence[int],
+                                            geometry: Geometry = KIMI_K3) -> torch.Tensor:
+    """Relabel a one-context-per-record partition so that
+    :func:`importance_group_order` visits records in ``record_order``."""
+
+    records = geometry.records
+    _validate_block_contexts(block_contexts, rate_transfer_mode(0, geometry) if geometry.records != 24
+                             else R0)
+    order = tuple(record_order)
+    if len(order) != records:
+        raise ValueError(f"record_order must contain {records} records")
+    if any(isinstance(r, bool) or not isinstance(r, int) or not 0 <= r < records for r in order) or len(set(order)) != records:
+        raise ValueError("record_order must be a permutation of all record IDs")
+    inverse = torch.empty(records, dtype=torch.long, device=block_contexts.device)
+    inverse[torch.tensor(order, dtype=torch.long, device=block_contexts.device)] = torch.arange(
+        records, device=block_contexts.device)
+    return inverse[block_contexts.to(torch.long)]
+
+
+def _validate_permutation(permutation: torch.Tensor, length: int, name: str = "permutation") -> None:
+    if permutation.ndim != 1 or permutation.numel() != length:
+        raise ValueError(f"{name} must contain exactly {length} entries")
+    if permutation.dtype == torch.bool or permutation.is_floating_point():
+        raise TypeError(f"{name} must use an integer dtype")
+    values = permutation.to(torch.long)
+    if not torch.equal(torch.sort(values).values, torch.arange(length, device=values.device)):
+        raise ValueError(f"{name} must be a bijection over 0..{length - 1}")
+
+
+def invert_permutation(permutation: torch.Tensor) -> torch.Tensor:
+    _validate_permutation(permutation, permutation.numel())
+    return torch.argsort(permutation.to(torch.long))
+
+
+def expand_group_order(group_order: torch.Tensor, geometry: Geometry = KIMI_K3) -> torch.Tensor:
+    """Four-channel group IDs -> new-channel -> old-channel permutation."""
+
+    groups = geometry.intermediate_channels // CONTEXT_GROUP_CHANNELS
+    if group_order.ndim != 1 or group_order.numel() != groups:
+        raise ValueError(f"group_order must contain {groups} groups")
+    _validate_permutation(group_order, groups, "group_order")
+    offsets = torch.arange(CONTEXT_GROUP_CHANNELS, device=group_order.device)
+    return (group_order.to(torch.long)[:, None] * CONTEXT_GROUP_CHANNELS + offsets[None]).flatten()
+
+
+def coupled_intermediate_permutation(w1: torch.Tensor, w3: torch.Tensor, w2: torch.Tensor,
+                                     permutation: torch.Tensor):
+    """One exact neuron permutation of an expert: ``w1[P]``, ``w3[P]``,
+    ``w2[:, P]`` (``permutation[new] = old``)."""
+
+    if w1.ndim != 2 or w3.ndim != 2 or w2.ndim != 2:
+        raise ValueError("expert weights must all be two-dimensional")
+    if w1.shape != w3.shape:
+        raise ValueError("w1 and w3 must have identical shapes")
+    intermediate, hidden = w1.shape
+    if tuple(w2.shape) != (hidden, intermediate):
+        raise ValueError("w2 must have shape [hidden, intermediate]")
+    _validate_permutation(permutation, intermediate)
+    p = permutation.to(torch.long)
+    return (w1.index_select(0, p.to(w1.device)).contiguous(), w3.index_select(0, p.to(w3.device)).contiguous(),
+            w2.index_select(1, p.to(w2.device)).contiguous())
+
+
+def record_repack_order(source_group_order: torch.Tensor, destination_group_order: torch.Tensor,
+                        geometry: Geometry = KIMI_K3) -> torch.Tensor:
+    """Destination record -> source record, refusing to split a record."""
+
+    groups = geometry.intermediate_channels // CONTEXT_GROUP_CHANNELS
+    _validate_permutation(source_group_order, groups, "source_group_order")
+    _validate_permutation(destination_group_order, groups, "destination_group_order")
+    per_record = geometry.record_channels // CONTEXT_GROUP_CHANNELS
+    src = source_group_order.cpu().reshape(-1, per_record)
+    dst = destination_group_order.cpu().reshape(-1, per_record)
+    lookup = {tuple(r.tolist()): i for i, r in enumerate(src)}
+    if len(lookup) != geometry.records:
+        raise ValueError("source order contains duplicate or malformed records")
+    try:
+        order = [lookup[tuple(r.tolist())] for r in dst]
+    except KeyError as exc:
+        raise ValueError("destination order splits or changes a source record") from exc
+    return torch.tensor(order, dtype=torch.long, device=source_group_order.device)
+
+
+def expand_record_order(record_order: torch.Tensor, geometry: Geometry = KIMI_K3) -> torch.Tensor:
+    _validate_permutation(record_order, geometry.records, "record_order")
+    offsets = torch.arange(geometry.record_channels, device=record_order.device)
+    return (record_order.to(torch.long)[:, None] * geometry.record_channels + offsets[None]).flatten()
+
+
+def repack_rate_axis(tensor: torch.Tensor, record_order: torch.Tensor, axis: int,
+                     geometry: Geometry = KIMI_K3) -> torch.Tensor:
+    """Move whole 128-channel blocks along a tensor's rate axis."""
+
+    if tensor.ndim == 0:
+        raise ValueError("cannot repack a scalar tensor")
+    axis = axis % tensor.ndim
+    if tensor.shape[axis] != geometry.intermediate_channels:
+        raise ValueError(f"rate axis must contain exactly {geometry.intermediate_channels} channels")
+    return tensor.index_select(axis, expand_record_order(record_order, geometry).to(tensor.device)).contiguous()
