@@ -285,6 +285,90 @@ def expert_bench(bits: int = 3, cpu_seconds: float = 4.0):
     }
 
 
+MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "f32": 157.3}
+
+
+def _time_ms(fn, steps: int) -> float:
+    """Mean duration of ``fn`` over ``steps`` launches, HIP events on the
+    current stream (the stream the kernels are launched on)."""
+
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def gemm_bench(steps: int = 5):
+    """The two MFMA GEMM shapes of the config-4 expert encode:
+    Hessian capture ``H += X^T X / n`` of 16,384 bf16 tokens x 7168 channels,
+    and one LDLQ span update ``P[:begin] += L[span, :begin]^T (W - Q)[span]``
+    (M = 7040, K = 128, N = 2048, FP32)."""
+
+    from qsrt_amd import gemm
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(20261201 + 6)
+    n, k = 16384, 7168
+    X = torch.randn((n, k), device=dev, generator=g).to(torch.bfloat16)
+    H = torch.zeros((k, k), device=dev)
+    ms_h = _time_ms(lambda: gemm.gram_(H, X, 1.0 / n), steps)
+    fl_h = 2.0 * n * k * k
+    del X, H
+    m, kk, nn = 7040, 128, 2048
+    L = torch.randn((kk, m), device=dev, generator=g)
+    W = torch.randn((kk, nn), device=dev, generator=g)
+    Q = torch.randn((kk, nn), device=dev, generator=g)
+    P = torch.zeros((m, nn), device=dev)
+    ms_l = _time_ms(lambda: gemm.addmm_sub_tn_(P, L, W, Q), steps)
+    fl_l = 2.0 * m * kk * nn
+    del L, W, Q, P
+    torch.cuda.empty_cache()
+
+    def line(name, ms, fl, dtype, shape):
+        t = fl / (ms / 1e3) / 1e12
+        return {"kernel": name, "shape": shape, "ms": round(ms, 4), "roofline": {
+            "bound": "mfma", "achieved": round(t, 1), "peak": MFMA_PEAK_TFLOPS[dtype], "unit": "TFLOP/s",
+            "frac": round(t / MFMA_PEAK_TFLOPS[dtype], 4), "traffic": None,
+            "algorithmic": f"2 M N K = {fl:.4g} flops/launch ({dtype} in, f32 accumulate)"}}
+
+    return {
+        "hessian_capture": line("gemm_tn_bf16_kernel", ms_h, fl_h, "bf16", f"X [{n} x {k}] bf16 -> H [{k} x {k}] f32"),
+        "ldlq_span_update": line("gemm_tn_f32_kernel", ms_l, fl_l, "f32",
+                                 f"L^T [{m} x {kk}] (W - Q) [{kk} x {nn}] f32"),
+    }
+
+
+def hadamard_bench(steps: int = 5):
+    """Block-128 rotation of a 7168 x 2048 FP32 matrix along each axis with
+    fused sign vectors (the ``su``/``sv`` sides of the expert's rotation):
+    8 B per element per launch."""
+
+    from qsrt_amd.hadamard import rotate_
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(20261201 + 7)
+    k, n = 7168, 2048
+    W = torch.randn((k, n), device=dev, generator=g)
+    su = torch.randint(0, 2, (k,), device=dev, generator=g).float() * 2 - 1
+    sv = torch.randint(0, 2, (n,), device=dev, generator=g).float() * 2 - 1
+    out = {}
+    for side, vec in (("left", su), ("right", sv)):
+        ms = _time_ms(lambda: rotate_(W, 128, side=side, pre_mul=vec), steps)
+        gbps = 8.0 * k * n / (ms / 1e3) / 1e9
+        out[side] = {"kernel": "hadamard_kernel", "ms": round(ms, 4), "roofline": {
+            "bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+            "algorithmic": f"8 B/element x {k * n} elements/launch"}}
+    del W
+    torch.cuda.empty_cache()
+    return {"workload": f"[{k} x {n}] f32, block 128, fused signs, in place", **out}
+
+
 def copy_calibration(nbytes: int) -> None:
     """A plain device copy of ``nbytes`` (the known-size reference for the
     HBM byte counters)."""
@@ -306,6 +390,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-expert", action="store_true", help="skip the config-4 expert encode")
     ap.add_argument("--no-decode", action="store_true", help="skip the layer decode")
+    ap.add_argument("--no-kernels", action="store_true", help="skip the GEMM and Hadamard kernel lines")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a device copy of BYTES (reference for HBM byte counters)")
     args = ap.parse_args()
@@ -405,6 +490,13 @@ def main() -> int:
         result["cpu_baseline"]["gpu_speedup"] = round(value / result["cpu_baseline"]["value"], 1)
     del tiles, outs
     torch.cuda.empty_cache()
+    if not args.no_kernels:
+        log("[bench] GEMM and Hadamard kernels")
+        result["gemm"] = gemm_bench()
+        result["hadamard"] = hadamard_bench()
+        log("[bench] gemm " + ", ".join(f"{k} {v['roofline']['achieved']} TFLOP/s" for k, v in result["gemm"].items())
+            + "; hadamard " + ", ".join(f"{k} {result['hadamard'][k]['roofline']['achieved']} GB/s"
+                                        for k in ("left", "right")))
     if not args.no_decode:
         log("[bench] layer decode")
         result["decode"] = decode_bench()
