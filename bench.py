@@ -317,7 +317,7 @@ def gemm_bench(steps: int = 5):
     X = torch.randn((n, k), device=dev, generator=g).to(torch.bfloat16)
     H = torch.zeros((k, k), device=dev)
     ms_h = _time_ms(lambda: gemm.gram_(H, X, 1.0 / n), steps)
-    fl_h = 2.0 * n * k * k
+    fl_h = 1.0 * n * k * (k + 1)  # symmetric rank-n update: one triangle computed, the other mirrored
     del X, H
     m, kk, nn = 7040, 128, 2048
     L = torch.randn((kk, m), device=dev, generator=g)
@@ -329,17 +329,18 @@ def gemm_bench(steps: int = 5):
     del L, W, Q, P
     torch.cuda.empty_cache()
 
-    def line(name, ms, fl, dtype, shape):
+    def line(name, ms, fl, dtype, shape, what):
         t = fl / (ms / 1e3) / 1e12
         return {"kernel": name, "shape": shape, "ms": round(ms, 4), "roofline": {
             "bound": "mfma", "achieved": round(t, 1), "peak": MFMA_PEAK_TFLOPS[dtype], "unit": "TFLOP/s",
             "frac": round(t / MFMA_PEAK_TFLOPS[dtype], 4), "traffic": None,
-            "algorithmic": f"2 M N K = {fl:.4g} flops/launch ({dtype} in, f32 accumulate)"}}
+            "algorithmic": f"{what} = {fl:.4g} flops/launch ({dtype} in, f32 accumulate)"}}
 
     return {
-        "hessian_capture": line("gemm_tn_bf16_kernel", ms_h, fl_h, "bf16", f"X [{n} x {k}] bf16 -> H [{k} x {k}] f32"),
+        "hessian_capture": line("gemm_tn_bf16_kernel", ms_h, fl_h, "bf16", f"X [{n} x {k}] bf16 -> H [{k} x {k}] f32",
+                                "n k (k + 1) (symmetric)"),
         "ldlq_span_update": line("gemm_tn_f32_kernel", ms_l, fl_l, "f32",
-                                 f"L^T [{m} x {kk}] (W - Q) [{kk} x {nn}] f32"),
+                                 f"L^T [{m} x {kk}] (W - Q) [{kk} x {nn}] f32", "2 M N K"),
     }
 
 

@@ -6,14 +6,16 @@
 //   qsrt/exl3_encoder_backend.py:496 and :534: prod_cache += L^T (W - Q)):
 //   v_mfma_f32_16x16x4_f32, exact FP32 products with FP32 accumulation; the
 //   subtraction W - Q is fused into the operand load (B2 may be NULL).
-// * bf16 operands (Hessian capture H += X^T X of BASELINE's kernel (c)):
+// * bf16 operands (Hessian capture H += X^T X / n, the H_data["H"] that
+//   qsrt/exl3_encoder_backend.py:2077-2122 finalises; the reference's in-tree
+//   accumulator, qsrt/kimi_reverse_pipeline.py:95-111, is an FP32 addmm_):
 //   v_mfma_f32_16x16x32_bf16 with FP32 accumulation; B2 must be NULL.
 //
-// One 256-thread workgroup per 128 x 128 tile of C (four waves of 64 x 64,
-// sixteen 16 x 16 MFMA tiles each).  K is walked in chunks staged through
-// LDS with double buffering: the next chunk's global loads are issued before
-// the current chunk's MFMAs.  Edges of M, N and K are zero-filled on load and
-// masked on store.
+// FP32: one 256-thread workgroup per 128 x 128 tile of C (four waves of
+// 64 x 64, sixteen 16 x 16 MFMA tiles each); K is walked in chunks staged
+// through LDS with double buffering, the next chunk's global loads issued
+// before the current chunk's MFMAs; edges of M, N and K are zero-filled on
+// load and masked on store.  bf16: see the comment above its kernel.
 
 #include "common.h"
 #include "qsrt_amd.h"
@@ -130,66 +132,160 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_f32_kernel(float* __restrict
 }
 
 // ---------------------------------------------------------------- bf16 path
-constexpr int kBK16 = 32;
-constexpr int kPad16 = 8;  // k-contiguous LDS rows: [m][k]
+// 256 x 256 tile of C per 512-thread workgroup (eight waves of 128 x 64:
+// 32 MFMA accumulators each), 64 k per stage.  Operands arrive k-major
+// ([k][m] in memory) but every MFMA fragment wants 8 consecutive k of one
+// m, so each thread loads an 8 k x 8 m unit with eight 16-byte loads,
+// transposes it in registers (v_perm on bf16 pairs) and writes eight
+// k-contiguous 16-byte rows to LDS; fragments are then single 16-byte LDS
+// reads.  LDS is double-buffered and the next stage's global loads are in
+// flight during the current stage's MFMAs: one barrier per stage.
+// With A == B (the Gram matrix X^T X) only tiles on and above the diagonal
+// run; off-diagonal tiles also add their transpose (float4 stores along m).
+constexpr int kT16 = 256;
+constexpr int kBK16 = 64;
+constexpr int kRow16 = kBK16 + 8;  // LDS row: 64 k + 8 pad (bf16) = 144 B
+constexpr int kThreads16 = 512;
 
-__global__ __launch_bounds__(kThreads) void gemm_tn_bf16_kernel(float* __restrict__ C, const uint16_t* __restrict__ A,
-                                                                const uint16_t* __restrict__ B, int64_t M, int64_t N,
-                                                                int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
-                                                                float alpha, int64_t tiles_n) {
-    // transposed staging: row = m (or n), 32 contiguous k per row
-    __shared__ __attribute__((aligned(16))) uint16_t As[kBM][kBK16 + kPad16];
-    __shared__ __attribute__((aligned(16))) uint16_t Bs[kBN][kBK16 + kPad16];
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct Bf16Unit {
+    u32x4 r[8];  // k-rows 8 ko + 0..7, columns 8 co + 0..7 (bf16 pairs)
+};
+
+// Eight k-rows of one 16-byte column group through a buffer resource that
+// ends at the last 16-byte group of valid columns of the stage's last row
+// (row min(K, k0 + 64) - 1): reads past it return zero (the K edge and the
+// last row's tail), so no load is predicated and nothing past the matrix is
+// read.  Columns past M or N in earlier rows read the following row; they
+// only feed rows or columns of C that are never stored.  `span` is the number
+// of columns from the tile's first column to the end of its valid 16-byte
+// groups.
+__device__ __forceinline__ void load_bf16(Bf16Unit& u, const uint16_t* P, int64_t k0, int64_t K, int64_t ld, int span,
+                                          int r0, int col) {
+    const int64_t left = K - k0;
+    const int rows = static_cast<int>(left < kBK16 ? left : kBK16);
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(P + k0 * ld), 0, ((rows - 1) * static_cast<int>(ld) + span) * 2, 0x00020000);
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+        u.r[r] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, ((r0 + r) * static_cast<int>(ld) + col) * 2, 0, 0);
+}
+
+// rows [8 co + e][8 ko .. 8 ko + 7] of the [column][k] LDS tile
+__device__ __forceinline__ void store_bf16(const Bf16Unit& u, uint16_t (*S)[kRow16], int co, int ko) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;  // high or low bf16 of each k-row word
+        u32x4 v;
+#pragma unroll
+        for (int kp = 0; kp < 4; ++kp) v[kp] = __builtin_amdgcn_perm(u.r[2 * kp + 1][e >> 1], u.r[2 * kp][e >> 1], sel);
+        *reinterpret_cast<u32x4*>(&S[8 * co + e][8 * ko]) = v;
+    }
+}
+
+template <bool SYM>
+__global__ __launch_bounds__(kThreads16) void gemm_tn_bf16_kernel(float* __restrict__ C, const uint16_t* __restrict__ A,
+                                                                  const uint16_t* __restrict__ B, int64_t M,
+                                                                  int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                                                                  int64_t ldc, float alpha, int tiles_n) {
+    __shared__ __attribute__((aligned(16))) uint16_t S[2][2][kT16][kRow16];  // [buffer][operand][column][k]
+    // Workgroup i runs on XCD i % 8: give every XCD a contiguous run of the tile order below, so the
+    // workgroups resident on one XCD at a time cover a compact 4 x 8 group of tiles and share 4 A and 8 B
+    // operand panels in that XCD's L2.  Tile order: groups row-major, tiles row-major inside a group; with
+    // SYM only tiles on or above the diagonal exist.
+    const unsigned nwg = gridDim.x, xcd = blockIdx.x % 8u, per = nwg / 8u, rem = nwg % 8u;
+    int rest = static_cast<int>(xcd * per + (xcd < rem ? xcd : rem) + blockIdx.x / 8u);
+    constexpr int GM = 4, GN = 8;
+    const int tiles_m = static_cast<int>((M + kT16 - 1) / kT16);
+    int tm = 0, tn = 0;
+    for (int gr = 0; gr * GM < tiles_m; ++gr) {
+        for (int gc = 0; gc * GN < tiles_n; ++gc) {
+            for (int i = 0; i < GM && gr * GM + i < tiles_m; ++i) {
+                const int row = gr * GM + i;
+                int lo = gc * GN, hi = gc * GN + GN < tiles_n ? gc * GN + GN : tiles_n;
+                if (SYM && lo < row) lo = row;
+                const int cnt = hi > lo ? hi - lo : 0;
+                if (rest < cnt) {
+                    tm = row;
+                    tn = lo + rest;
+                    goto found;
+                }
+                rest -= cnt;
+            }
+        }
+    }
+    return;  // not reached: the grid holds exactly the tiles of the order
+found:
+    const int64_t m0 = static_cast<int64_t>(tm) * kT16, n0 = static_cast<int64_t>(tn) * kT16;
+
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int c = lane & 15, g = lane >> 4;
-    const int64_t m0 = (blockIdx.x / tiles_n) * kBM, n0 = (blockIdx.x % tiles_n) * kBN;
-    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
+    // staging unit of this thread: operand op (uniform per wave), column octet co, k octet ko
+    const int op = __builtin_amdgcn_readfirstlane(t >> 8), u = t & 255, co = u & 31, ko = u >> 5;
+    const uint16_t* P = op ? B + n0 : A + m0;
+    const int64_t pld = op ? ldb : lda, pcols = op ? N : M, pc0 = op ? n0 : m0;
+    const int64_t pend = ((pcols + 7) & ~int64_t{7}) < pld ? ((pcols + 7) & ~int64_t{7}) : pld;
+    const int span = static_cast<int>(pend - pc0);
 
-    f32x4 acc[4][4];
+    f32x4 acc[8][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 8; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int64_t k0 = 0; k0 < K; k0 += kBK16) {
-        // 32 k-rows x 128 columns per operand: thread t takes k-row t / 8, columns 16 (t % 8) .. +15
-        const int r = t >> 3, q = (t & 7) * 16;
-        const int64_t krow = k0 + r;
+    const int64_t stages = (K + kBK16 - 1) / kBK16;
+    Bf16Unit unit;
+    load_bf16(unit, P, 0, K, pld, span, 8 * ko, 8 * co);
+    store_bf16(unit, S[0][op], co, ko);
+    if (stages > 1) load_bf16(unit, P, kBK16, K, pld, span, 8 * ko, 8 * co);
+    __syncthreads();
+    for (int64_t s = 0; s < stages; ++s) {
+        const int cur = static_cast<int>(s & 1);
 #pragma unroll
-        for (int op = 0; op < 2; ++op) {
-            const uint16_t* P = op == 0 ? A : B;
-            const int64_t cols = op == 0 ? M : N, base = op == 0 ? m0 : n0, ld = op == 0 ? lda : ldb;
-            uint16_t (*S)[kBK16 + kPad16] = op == 0 ? As : Bs;
+        for (int kk = 0; kk < kBK16; kk += 32) {
+            bf16x8 a[8], b[4];
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int64_t col = base + q + e;
-                S[q + e][r] = (krow < K && col < cols) ? P[krow * ld + col] : static_cast<uint16_t>(0);
-            }
+            for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const bf16x8*>(&S[cur][0][wm + 16 * i + c][kk + 8 * g]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const bf16x8*>(&S[cur][1][wn + 16 * j + c][kk + 8 * g]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
         }
-        __syncthreads();
-        bf16x8 a[4], b[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const bf16x8*>(&As[wm + 16 * i + c][8 * g]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const bf16x8*>(&Bs[wn + 16 * j + c][8 * g]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+        if (s + 1 < stages) store_bf16(unit, S[cur ^ 1][op], co, ko);
+        if (s + 2 < stages) load_bf16(unit, P, (s + 2) * kBK16, K, pld, span, 8 * ko, 8 * co);
         __syncthreads();
     }
+
+    // lane holds C[m0 + wm + 16 i + 4 g + r][n0 + wn + 16 j + c], r = 0..3
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 8; ++i) {
+        const int64_t row0 = m0 + wm + 16 * i + 4 * g;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int64_t row = m0 + wm + 16 * i + 4 * g + r;
-            if (row >= M) continue;
+        for (int j = 0; j < 4; ++j) {
+            const int64_t col = n0 + wn + 16 * j + c;
+            if (col >= N) continue;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int64_t col = n0 + wn + 16 * j + c;
-                if (col < N) C[row * ldc + col] += alpha * acc[i][j][r];
+            for (int r = 0; r < 4; ++r)
+                if (row0 + r < M) C[(row0 + r) * ldc + col] += alpha * acc[i][j][r];
+            if (SYM && tm != tn) {  // the transposed tile: C[col][row0 .. row0 + 3]
+                float* q = C + col * ldc + row0;
+                if (row0 + 3 < M) {
+                    f32x4 v = *reinterpret_cast<const f32x4*>(q);
+                    v += alpha * acc[i][j];
+                    *reinterpret_cast<f32x4*>(q) = v;
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (row0 + r < M) q[r] += alpha * acc[i][j][r];
+                }
             }
         }
+    }
 }
 
 }  // namespace
@@ -217,9 +313,22 @@ int qsrt_gemm_tn(float* C, const void* A, const void* B, const void* B2, int64_t
                            M, N, K, lda, ldb, ldc, alpha, tiles_n);
     } else {
         if (B2) return qsrt::fail(qsrt::kBadArgument, "the bf16 path has no fused subtraction");
-        hipLaunchKernelGGL(gemm_tn_bf16_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, stream, C,
-                           static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(B), M, N, K, lda, ldb, ldc,
-                           alpha, tiles_n);
+        if (lda % 8 || ldb % 8 || reinterpret_cast<uintptr_t>(A) % 16 || reinterpret_cast<uintptr_t>(B) % 16)
+            return qsrt::fail(qsrt::kBadArgument, "bf16 operands must be 16-byte aligned with lda, ldb multiples of 8");
+        if (lda > (1 << 23) || ldb > (1 << 23))
+            return qsrt::fail(qsrt::kBadArgument, "bf16 leading dimensions above 2^23 are not supported");
+        const int64_t tm = (M + kT16 - 1) / kT16, tn = (N + kT16 - 1) / kT16;
+        const bool sym = A == B && lda == ldb && M == N && ldc % 4 == 0 && reinterpret_cast<uintptr_t>(C) % 16 == 0;
+        const int64_t n = sym ? tm * (tm + 1) / 2 : tm * tn;
+        if (n > 0x7fffffff || tn > 0x7fffffff) return qsrt::fail(qsrt::kBadArgument, "GEMM too large for one launch");
+        if (sym)
+            hipLaunchKernelGGL(gemm_tn_bf16_kernel<true>, dim3(static_cast<unsigned>(n)), dim3(kThreads16), 0, stream,
+                               C, static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(B), M, N, K, lda, ldb,
+                               ldc, alpha, static_cast<int>(tn));
+        else
+            hipLaunchKernelGGL(gemm_tn_bf16_kernel<false>, dim3(static_cast<unsigned>(n)), dim3(kThreads16), 0,
+                               stream, C, static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(B), M, N, K,
+                               lda, ldb, ldc, alpha, static_cast<int>(tn));
     }
     QSRT_HIP_TRY(hipGetLastError());
     return qsrt::kOk;

@@ -36,14 +36,14 @@ def _copy_padded(t: torch.Tensor, ld: int) -> torch.Tensor:
     return view
 
 
-def _aligned(t: torch.Tensor) -> torch.Tensor:
+def _aligned(t: torch.Tensor, multiple: int = 4) -> torch.Tensor:
     """``t`` as a row-major matrix with a 16-byte aligned base and a leading
-    dimension that is a multiple of 4 elements (copied into a padded buffer
-    when needed)."""
+    dimension that is a multiple of ``multiple`` elements (copied into a
+    padded buffer when needed): the kernels read 16 bytes at a time."""
 
-    if _row_major(t) and t.data_ptr() % 16 == 0 and t.stride(0) % 4 == 0:
+    if _row_major(t) and t.data_ptr() % 16 == 0 and t.stride(0) % multiple == 0:
         return t
-    return _copy_padded(t, (t.shape[1] + 3) // 4 * 4)
+    return _copy_padded(t, (t.shape[1] + multiple - 1) // multiple * multiple)
 
 
 def addmm_sub_tn_(C: torch.Tensor, A: torch.Tensor, B: torch.Tensor, B2: torch.Tensor | None = None,
@@ -92,10 +92,13 @@ def gram_(H: torch.Tensor, X: torch.Tensor, alpha: float = 1.0) -> torch.Tensor:
     if H.shape != (k, k) or H.dtype != torch.float32:
         raise ValueError("gram_: H must be float32 [k, k]")
     if H.is_cuda:
-        X = X.contiguous()
+        if not _row_major(H):
+            raise ValueError("gram_: H must be row-major")
         if X.dtype == torch.bfloat16:
+            X = _aligned(X, 8)
             _launch(H, X, X, None, alpha, 1)
         elif X.dtype == torch.float32:
+            X = _aligned(X)
             _launch(H, X, X, None, alpha, 0)
         else:
             raise ValueError("gram_: X must be bfloat16 or float32")

@@ -56,18 +56,39 @@ def test_strided_ldlq_views():
     assert _rel(comp.cpu().double().numpy(), want) < 1e-5
 
 
-@pytest.mark.parametrize("n,k", [(4096, 256), (1000, 200)])
+@pytest.mark.parametrize("n,k", [(4096, 256), (1000, 200), (777, 600), (130, 203), (64, 8), (3, 520)])
 def test_bf16_gram_matches_float64(n, k):
+    """Symmetric path: tiles on and above the diagonal plus their mirror;
+    ragged k (padded leading dimension), ragged n (zero-filled K edge) and an
+    accumulated, non-zero H."""
+
     print(f"[gemm] bf16 gram n{n} k{k}", file=sys.stderr, flush=True)
     g = torch.Generator().manual_seed(n + k)
     X = torch.randn(n, k, generator=g).bfloat16()
-    H = torch.zeros(k, k).cuda()
+    H0 = torch.randn(k, k, generator=g)
+    H = H0.cuda()
     gemm.gram_(H, X.cuda(), alpha=1.0 / n)
     x64 = X.double().numpy()
-    assert _rel(H.cpu().double().numpy(), x64.T @ x64 / n) < 1e-5
+    want = H0.double().numpy() + x64.T @ x64 / n
+    assert _rel(H.cpu().double().numpy(), want) < 1e-5
     Hf = torch.zeros(k, k).cuda()
     gemm.gram_(Hf, X.float().cuda())
     assert _rel(Hf.cpu().double().numpy(), x64.T @ x64) < 1e-5
+
+
+@pytest.mark.parametrize("K,M,N", [(1000, 520, 264), (64, 256, 256), (129, 8, 600)])
+def test_bf16_general_product_matches_float64(K, M, N):
+    """Distinct operands take the full tile grid (no mirroring)."""
+
+    print(f"[gemm] bf16 general K{K} M{M} N{N}", file=sys.stderr, flush=True)
+    g = torch.Generator().manual_seed(K + M + N)
+    A = torch.randn(K, M, generator=g).bfloat16()
+    B = torch.randn(K, N, generator=g).bfloat16()
+    C0 = torch.randn(M, N, generator=g)
+    C = C0.cuda()
+    gemm._launch(C, gemm._aligned(A.cuda(), 8), gemm._aligned(B.cuda(), 8), None, 0.25, 1)
+    want = C0.double().numpy() + 0.25 * (A.double().numpy().T @ B.double().numpy())
+    assert _rel(C.cpu().double().numpy(), want) < 1e-5
 
 
 def test_gemm_rejects_bad_arguments():
