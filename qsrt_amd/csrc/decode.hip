@@ -1,6 +1,8 @@
 // Fused trellis decode: packed EXL words -> cyclic states -> E4M3 labels ->
 // W = diag(su) . H128 X H128 . diag(sv) -> bf16 (or f32), one 128x128 block
-// per workgroup iteration.
+// per workgroup iteration.  Each workgroup walks a contiguous run of blocks
+// (runs differ by at most one block); the block cursor advances by carries,
+// with no per-block division.
 //
 // Reference semantics (qsrt/exl3_reference.py:61-302, qsrt/qsrt.py:1175-1209):
 //   X[K, N]  = labels of the states, tile-major, tensor-core order in a tile
@@ -41,6 +43,8 @@
 // Tables whose labels exceed 6 in magnitude use FP32 MFMAs for both products
 // (labels widened exactly to FP32), with the same data movement.
 
+#include <algorithm>
+
 #include "common.h"
 #include "qsrt_amd.h"
 
@@ -66,10 +70,34 @@ struct Job {
     const float* col_scale;
     void* out;
     int64_t out_ld;
-    int64_t rows;
-    int64_t cols;
+    int32_t nbr, nbc;     // 128 x 128 blocks along rows and columns (both > 0)
     int64_t first_block;  // prefix over jobs (filled by the host)
 };
+
+// Position of a workgroup in its run of blocks: job and block coordinates,
+// all wave-uniform.  Runs are contiguous, so moving to the next block is a
+// carry chain instead of a division.
+struct Cursor {
+    int j, br, bc;
+};
+
+__device__ __forceinline__ Cursor cursor_at(const Job* jobs, int n_jobs, int64_t blk) {
+    int j = 0;
+    while (j + 1 < n_jobs && jobs[j + 1].first_block <= blk) ++j;
+    const int64_t local = blk - jobs[j].first_block;
+    const int br = static_cast<int>(local / jobs[j].nbc);
+    return Cursor{j, br, static_cast<int>(local - static_cast<int64_t>(br) * jobs[j].nbc)};
+}
+
+__device__ __forceinline__ void cursor_next(const Job* jobs, Cursor& cu) {
+    if (++cu.bc == jobs[cu.j].nbc) {
+        cu.bc = 0;
+        if (++cu.br == jobs[cu.j].nbr) {
+            cu.br = 0;
+            ++cu.j;
+        }
+    }
+}
 
 struct BlockCtx {
     const int16_t* words;  // tile (8 br, 8 bc) of the block
@@ -80,19 +108,15 @@ struct BlockCtx {
     int64_t ld;
 };
 
-__device__ __forceinline__ BlockCtx block_ctx(const Job* jobs, int n_jobs, int& j, int64_t blk, int out_size) {
-    while (j + 1 < n_jobs && jobs[j + 1].first_block <= blk) ++j;
-    const Job& J = jobs[j];
-    const int64_t local = blk - J.first_block;
-    const int64_t nbc = J.cols >> 7;
-    const int64_t br = local / nbc, bc = local - br * nbc;
+__device__ __forceinline__ BlockCtx block_ctx(const Job* jobs, const Cursor& cu, int out_size) {
+    const Job& J = jobs[cu.j];
     BlockCtx x;
-    x.words = J.words + 8 * br * J.tile_row_stride + 8 * bc * J.tile_col_stride;
+    x.words = J.words + 8 * (cu.br * J.tile_row_stride + cu.bc * J.tile_col_stride);
     x.trs = J.tile_row_stride;
     x.tcs = J.tile_col_stride;
-    x.su = J.row_scale + 128 * br;
-    x.sv = J.col_scale + 128 * bc;
-    x.out = static_cast<char*>(J.out) + (128 * br * J.out_ld + 128 * bc) * out_size;
+    x.su = J.row_scale + 128 * cu.br;
+    x.sv = J.col_scale + 128 * cu.bc;
+    x.out = static_cast<char*>(J.out) + (128 * cu.br * J.out_ld + 128 * cu.bc) * out_size;
     x.ld = J.out_ld;
     return x;
 }
@@ -121,6 +145,11 @@ void decode_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t total_block
     // slice [2 KB w, 2 KB (w + 1)) also stages its packed words (phase A) and
     // its outputs (phase B2), when no other wave reads it.
     __shared__ __attribute__((aligned(16))) uint8_t labels[kLabelBytes];
+
+    // this workgroup's run of blocks: [begin, end), sizes differ by at most one
+    const int64_t begin = total_blocks * blockIdx.x / gridDim.x;
+    const int64_t end = total_blocks * (blockIdx.x + 1) / gridDim.x;
+    if (begin >= end) return;
 
     for (int i = threadIdx.x; i < 65536 / 16; i += kThreads)
         reinterpret_cast<uint4*>(lut_s)[i] = reinterpret_cast<const uint4*>(lut)[i];
@@ -164,57 +193,60 @@ void decode_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t total_block
 #pragma unroll
     for (int q = 0; q < 4; ++q) asm volatile("" : "+v"(hr[q]));
 
+    // The lane's 16 + 3K-bit window starts at stream bit b0; sh = b0 % 32 is never 0 for K = 2, 3, 4 and these
+    // positions (b0 = (p0 + 1) K - 16 with p0 = 32 (c % 8) + 8 g + 4 (c / 8)), so one funnel shift extracts it.
     const int p0 = 32 * (c & 7) + 8 * g + 4 * (c >> 3);
     int b0 = (p0 + 1) * K - 16;
     if (b0 < 0) b0 += 256 * K;
     const int m0 = b0 >> 5;
     const int m1 = (m0 + 1) % (8 * K);
-    const int sh = b0 & 31;
+    const uint32_t rsh = 32u - static_cast<uint32_t>(b0 & 31);
 
     uint8_t* slice = labels + 2048 * w;
     uint4* lab_w = reinterpret_cast<uint4*>(labels) + (w * 2) * 64 + lane;
     const uint4* lab_r = reinterpret_cast<const uint4*>(labels) + lane;
     const uint32_t* wstage = reinterpret_cast<const uint32_t*>(slice);
 
-    int job = 0;
-    int64_t blk = blockIdx.x;
-    u32x4 words = {0u, 0u, 0u, 0u};
-    float su = 0.f, sv[8];
-    BlockCtx ctx{};
-    if (blk < total_blocks) {
-        ctx = block_ctx(jobs, n_jobs, job, blk, sizeof(OutT));
-        words = fetch_words<K>(ctx, w, lane);
-        su = ((gf32)ctx.su)[16 * w + c];
+    Cursor cu = cursor_at(jobs, n_jobs, begin);
+    BlockCtx ctx = block_ctx(jobs, cu, sizeof(OutT));
+    u32x4 words = fetch_words<K>(ctx, w, lane);
+    float su = ((gf32)ctx.su)[16 * w + c];
+    float sv[8];
 #pragma unroll
-        for (int a = 0; a < 8; ++a) sv[a] = ((gf32)ctx.sv)[16 * a + c];
-    }
+    for (int a = 0; a < 8; ++a) sv[a] = ((gf32)ctx.sv)[16 * a + c];
     __syncthreads();
 
-    for (; blk < total_blocks; blk += gridDim.x) {
+    for (int64_t blk = begin; blk < end; ++blk) {
         // ---- A: stage the tile-column's words, decode the lane's labels
         if (lane < 16 * K) reinterpret_cast<u32x4*>(slice)[lane] = words;
         uint32_t lab[8];
 #pragma unroll
         for (int a = 0; a < 8; ++a) {
             const uint32_t lo = wstage[a * 8 * K + m0], hi = wstage[a * 8 * K + m1];
-            const uint64_t two = (static_cast<uint64_t>(lo) << 32) | hi;
-            const uint32_t win = static_cast<uint32_t>(two >> (32 - sh));
-            const uint32_t v01 = lut_s[(win >> 16) & 0xFFFFu] | (static_cast<uint32_t>(lut_s[(win >> (16 - K)) & 0xFFFFu]) << 16);
+            const uint32_t win = __builtin_amdgcn_alignbit(lo, hi, rsh);  // stream bits [b0, b0 + 32)
+            const uint32_t v01 = lut_s[win >> 16] | (static_cast<uint32_t>(lut_s[(win >> (16 - K)) & 0xFFFFu]) << 16);
             const uint32_t v23 = lut_s[(win >> (16 - 2 * K)) & 0xFFFFu] |
                                  (static_cast<uint32_t>(lut_s[(win >> (16 - 3 * K)) & 0xFFFFu]) << 16);
             lab[a] = __builtin_amdgcn_perm(v23, v01, 0x06040200u);
         }
         lab_w[0] = make_uint4(lab[0], lab[1], lab[2], lab[3]);
         lab_w[64] = make_uint4(lab[4], lab[5], lab[6], lab[7]);
-        // ---- prefetch the next block (before this block's stores)
-        const BlockCtx cur = ctx;
-        const float su_cur = su;
-        float sv_cur[8];
+        // this block's scale operands, before the prefetch below replaces su and sv
+        uint32_t sv2[8];  // FP8 path: fp16 pairs
+        float svf[8];     // FP32 path
 #pragma unroll
-        for (int a = 0; a < 8; ++a) sv_cur[a] = sv[a];
-        const int64_t nb = blk + gridDim.x;
-        if (nb < total_blocks) {
-            ctx = block_ctx(jobs, n_jobs, job, nb, sizeof(OutT));
+        for (int a = 0; a < 8; ++a) {
+            if constexpr (FP8)
+                sv2[a] = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(sv[a]), static_cast<_Float16>(sv[a])});
+            else
+                svf[a] = sv[a];
+        }
+        const float su_cur = su;
+        const BlockCtx cur = ctx;
+        // ---- prefetch the next block (before this block's stores)
+        if (blk + 1 < end) {
+            cursor_next(jobs, cu);
+            ctx = block_ctx(jobs, cu, sizeof(OutT));
             words = fetch_words<K>(ctx, w, lane);
             su = ((gf32)ctx.su)[16 * w + c];
 #pragma unroll
@@ -285,8 +317,7 @@ void decode_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t total_block
                         bv[q + 4] = static_cast<_Float16>(ev - hi32);
                     }
                     // A rows: +-sv of the output column (sign bits from H16 via XOR)
-                    const uint32_t sv2 = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(sv_cur[a]), static_cast<_Float16>(sv_cur[a])});
-                    const uint32_t a01 = sv2 ^ hsg[0], a23 = sv2 ^ hsg[1];
+                    const uint32_t a01 = sv2[a] ^ hsg[0], a23 = sv2[a] ^ hsg[1];
                     typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
                     const u32x4v araw = {a01, a23, a01, a23};
                     const f16x8 avh = __builtin_bit_cast(f16x8, araw);
@@ -294,7 +325,7 @@ void decode_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t total_block
                 } else {
 #pragma unroll
                     for (int q = 0; q < 4; ++q)
-                        d = __builtin_amdgcn_mfma_f32_16x16x4f32(hr[q] * sv_cur[a], e[a][q], d, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x4f32(hr[q] * svf[a], e[a][q], d, 0, 0, 0);
                 }
                 d = d * su_cur;
                 // row c, staged columns 16 t + 4 g .. +3 -> byte offset, 16-byte chunks XOR-swizzled by row
@@ -323,12 +354,15 @@ void decode_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t total_block
 }
 
 template <int K, bool FP8>
-void launch(const Job* jobs, int n_jobs, int64_t total, const uint8_t* lut, int out_dtype, unsigned grid,
+void launch(const Job* jobs, int n_jobs, int64_t total, const uint8_t* lut, int out_dtype, int cus,
             hipStream_t stream) {
+    const unsigned grid = static_cast<unsigned>(std::min<int64_t>(2 * static_cast<int64_t>(cus), total));  // 2 per CU
     if (out_dtype == 0)
-        hipLaunchKernelGGL((decode_kernel<K, FP8, __bf16>), dim3(grid), dim3(kThreads), 0, stream, jobs, n_jobs, total, lut);
+        hipLaunchKernelGGL((decode_kernel<K, FP8, __bf16>), dim3(grid), dim3(kThreads), 0, stream, jobs, n_jobs, total,
+                           lut);
     else
-        hipLaunchKernelGGL((decode_kernel<K, FP8, float>), dim3(grid), dim3(kThreads), 0, stream, jobs, n_jobs, total, lut);
+        hipLaunchKernelGGL((decode_kernel<K, FP8, float>), dim3(grid), dim3(kThreads), 0, stream, jobs, n_jobs, total,
+                           lut);
 }
 
 }  // namespace
@@ -356,6 +390,7 @@ int qsrt_decode(const qsrt_decode_job* jobs, int n_jobs, int K, const uint8_t* l
     Job* host = static_cast<Job*>(malloc(sizeof(Job) * n_jobs));
     if (!host) return qsrt::fail(qsrt::kHipError, "host allocation failed");
     int64_t total = 0;
+    int kept = 0;
     for (int i = 0; i < n_jobs; ++i) {
         const qsrt_decode_job& s = jobs[i];
         const bool ok = s.words && s.row_scale && s.col_scale && s.out && s.rows >= 0 && s.cols >= 0 &&
@@ -363,34 +398,42 @@ int qsrt_decode(const qsrt_decode_job* jobs, int n_jobs, int K, const uint8_t* l
                         reinterpret_cast<uintptr_t>(s.words) % 16 == 0 && s.tile_row_stride % 8 == 0 &&
                         s.tile_col_stride % 8 == 0 && reinterpret_cast<uintptr_t>(s.out) % 16 == 0 &&
                         s.out_ld % 8 == 0 &&
-                        reinterpret_cast<uintptr_t>(s.col_scale) % 16 == 0;
+                        reinterpret_cast<uintptr_t>(s.col_scale) % 16 == 0 &&
+                        reinterpret_cast<uintptr_t>(s.row_scale) % 16 == 0;
         if (!ok) {
             free(host);
             return qsrt::fail(qsrt::kBadArgument,
                               "decode job %d: need rows, cols multiples of 128, out_ld >= cols and a multiple of 8, "
-                              "16-byte aligned words, out and col_scale, tile strides multiples of 8, non-null pointers",
+                              "16-byte aligned words, out, row_scale and col_scale, tile strides multiples of 8, non-null pointers",
                               i);
         }
-        host[i] = Job{s.words, s.tile_row_stride, s.tile_col_stride, s.row_scale, s.col_scale, s.out, s.out_ld,
-                      s.rows, s.cols, total};
+        if (s.rows / 128 >= (1 << 30) || s.cols / 128 >= (1 << 30)) {
+            free(host);
+            return qsrt::fail(qsrt::kBadArgument, "decode job %d is too large", i);
+        }
+        if (s.rows == 0 || s.cols == 0) continue;  // nothing to decode; the kernel never sees empty jobs
+        host[kept++] = Job{s.words, s.tile_row_stride, s.tile_col_stride, s.row_scale, s.col_scale, s.out, s.out_ld,
+                           static_cast<int32_t>(s.rows / 128), static_cast<int32_t>(s.cols / 128), total};
         total += (s.rows / 128) * (s.cols / 128);
     }
-    const hipError_t cp = hipMemcpyAsync(workspace, host, sizeof(Job) * n_jobs, hipMemcpyHostToDevice, stream);
+    if (kept == 0) {
+        free(host);
+        return qsrt::kOk;
+    }
+    const hipError_t cp = hipMemcpyAsync(workspace, host, sizeof(Job) * kept, hipMemcpyHostToDevice, stream);
     free(host);
     if (cp != hipSuccess) return qsrt::fail(qsrt::kHipError, "job upload failed: %s", hipGetErrorString(cp));
     if (total == 0) return qsrt::kOk;
     int cus = 0;
     if (const int rc = qsrt::current_cu_count(&cus)) return rc;
-    const int64_t slots = 2 * static_cast<int64_t>(cus);  // two workgroups per CU
-    const unsigned grid = static_cast<unsigned>(total < slots ? total : slots);
     const Job* dj = static_cast<const Job*>(workspace);
     switch (K * 2 + (exact_fp8 ? 1 : 0)) {
-        case 5: launch<2, true>(dj, n_jobs, total, lut_e4m3, out_dtype, grid, stream); break;
-        case 4: launch<2, false>(dj, n_jobs, total, lut_e4m3, out_dtype, grid, stream); break;
-        case 7: launch<3, true>(dj, n_jobs, total, lut_e4m3, out_dtype, grid, stream); break;
-        case 6: launch<3, false>(dj, n_jobs, total, lut_e4m3, out_dtype, grid, stream); break;
-        case 9: launch<4, true>(dj, n_jobs, total, lut_e4m3, out_dtype, grid, stream); break;
-        default: launch<4, false>(dj, n_jobs, total, lut_e4m3, out_dtype, grid, stream); break;
+        case 5: launch<2, true>(dj, kept, total, lut_e4m3, out_dtype, cus, stream); break;
+        case 4: launch<2, false>(dj, kept, total, lut_e4m3, out_dtype, cus, stream); break;
+        case 7: launch<3, true>(dj, kept, total, lut_e4m3, out_dtype, cus, stream); break;
+        case 6: launch<3, false>(dj, kept, total, lut_e4m3, out_dtype, cus, stream); break;
+        case 9: launch<4, true>(dj, kept, total, lut_e4m3, out_dtype, cus, stream); break;
+        default: launch<4, false>(dj, kept, total, lut_e4m3, out_dtype, cus, stream); break;
     }
     QSRT_HIP_TRY(hipGetLastError());
     return qsrt::kOk;
