@@ -194,26 +194,39 @@ def cpu_baseline(tiles_np, seconds_target: float = 12.0):
     }
 
 
-DECODE_MATRICES = 1152  # 384 experts x 3 matrices of the Kimi-class shape
+DECODE_EXPERTS = 384  # a layer of Kimi-class experts
+# Per-matrix record rates of the decoded layer: H308's 2 K4 + 22 K3 needs 24 records; the 7168 x 2048 expert has
+# 16 records of 128 intermediate channels, so its record-granular analogue is 2 K4 + 14 K3 (3.125 trellis bpw).
+DECODE_RECORD_BITS = (3,) * 14 + (4,) * 2
 HBM_PEAK_GBPS = 8000.0
 
 
-def decode_bench(steps: int = 3, matrices: int = DECODE_MATRICES, bits: int = 3):
-    """Whole-layer decode (BASELINE config 5 shape): ``matrices`` packed
-    7168 x 2048 trellis payloads at rate ``bits`` -> bf16, one launch.
+def decode_bench(steps: int = 3, experts: int = DECODE_EXPERTS):
+    """Whole-layer decode: ``experts`` x (gate, up, down)
+    record-major payloads with mixed record rates -> bf16.  Gate/up
+    [7168 x 2048] carry their records along N, down [2048 x 7168] along K, as
+    the encoder stores them.  One prepared plan, one launch per rate per step.
     Payload words are random (any word stream is a valid cyclic path)."""
 
     from qsrt_amd.decode import DecodePlan
     from qsrt_amd.sqg_e4m3 import sqg_xor_cheb_t12_bytes
 
     dev = torch.device("cuda:0")
-    k, n = 7168, 2048
+    h, i = 7168, 2048
+    bits = DECODE_RECORD_BITS
+    words_per = h * i * sum(bits) // (16 * len(bits))
+    n_mat = 3 * experts
     g = torch.Generator(device=dev).manual_seed(20261201 + 5)
-    words = torch.randint(-32768, 32767, (matrices, k // 16, n // 16, 16 * bits), dtype=torch.int16, device=dev, generator=g)
-    su = (torch.rand(k, device=dev, generator=g) + 0.5) / 128.0
-    sv = torch.rand(n, device=dev, generator=g) - 0.5
-    out = torch.empty((matrices, k, n), dtype=torch.bfloat16, device=dev)
-    plan = DecodePlan([(words[i], su, sv, out[i]) for i in range(matrices)], bits, sqg_xor_cheb_t12_bytes(bits))
+    words = torch.randint(-32768, 32767, (n_mat, words_per), dtype=torch.int16, device=dev, generator=g)
+    su = (torch.rand((n_mat, 7168), device=dev, generator=g) + 0.5) / 128.0
+    sv = torch.rand((n_mat, 7168), device=dev, generator=g) - 0.5
+    out = torch.empty((n_mat, h * i), dtype=torch.bfloat16, device=dev)
+    payloads = []
+    for m in range(n_mat):
+        down = m % 3 == 2
+        k, n = (i, h) if down else (h, i)
+        payloads.append((words[m], bits, "k" if down else "n", su[m, :k], sv[m, :n], out[m].view(k, n)))
+    plan = DecodePlan.for_records(payloads, {b: sqg_xor_cheb_t12_bytes(b).to(dev) for b in set(bits)})
     plan.run()
     torch.cuda.synchronize()
     ms = []
@@ -224,14 +237,16 @@ def decode_bench(steps: int = 3, matrices: int = DECODE_MATRICES, bits: int = 3)
         e1.record()
         torch.cuda.synchronize()
         ms.append(e0.elapsed_time(e1))
-    weights = matrices * k * n
-    byts = weights * (bits / 8 + 2) + matrices * (k + n) * 4
+    weights = n_mat * h * i
+    bpw = sum(bits) / len(bits)
+    byts = weights * (bpw / 8 + 2) + n_mat * (h + i) * 4
     t = min(ms) / 1e3
-    del words, out
+    del words, out, plan, payloads
     torch.cuda.empty_cache()
     return {
-        "workload": f"{matrices} x [{k} x {n}] K{bits} payloads -> bf16 (one launch, config-5 layer shape)",
-        "kernel": "decode_kernel",
+        "workload": f"config 5 layer: {experts} experts x (gate, up [{h} x {i}], down [{i} x {h}]), records "
+                    f"{bits.count(3)} K3 + {bits.count(4)} K4 ({bpw:.3f} trellis bpw) -> bf16",
+        "kernel": "decode_kernel (one launch per rate)",
         "ms": round(min(ms), 3),
         "G_weights_per_s": round(weights / t / 1e9, 2),
         "roofline": {
@@ -241,7 +256,8 @@ def decode_bench(steps: int = 3, matrices: int = DECODE_MATRICES, bits: int = 3)
             "unit": "GB/s",
             "frac": round(byts / t / 1e9 / HBM_PEAK_GBPS, 4),
             "traffic": round(byts * DECODE_TRAFFIC_OVER_ALGORITHMIC),
-            "algorithmic": f"{bits}/8 B payload + 2 B bf16 out per weight + (K + N) f32 scales per matrix = {byts} B/launch",
+            "algorithmic": f"{bpw:.3f}/8 B payload + 2 B bf16 out per weight + (K + N) f32 scales per matrix "
+                           f"= {byts:.4g} B per layer (both launches)",
         },
     }
 

@@ -93,11 +93,15 @@ int qsrt_hadamard(float *x, int64_t rows, int64_t cols, int64_t ld, int block, i
                   const float *pre_div, const float *post_mul, void *stream);
 
 /*
- * One matrix (or one record strip of a mixed-rate matrix) for qsrt_decode.
- * Tile (r, c) of the [rows/16, cols/16] tile grid starts at
- *   words + r * tile_row_stride + c * tile_col_stride   (int16 elements)
- * and holds 16 K int16 EXL words.  Output element (i, j) is written to
- *   out[i * out_ld + j] = row_scale[i] * col_scale[j] * (H X H)[i][j]
+ * One matrix (or a run of record strips of a mixed-rate matrix) for
+ * qsrt_decode.  The matrix is a grid of 128 x 128 blocks of 8 x 8 tiles;
+ * tile (i, j) of block (R, C) starts at
+ *   words + R * block_row_stride + C * block_col_stride
+ *         + i * tile_row_stride + j * tile_col_stride      (int16 elements)
+ * (block strides of 0 mean 8 * tile_row_stride and 8 * tile_col_stride: a
+ * plain tile grid) and holds 16 K int16 EXL words.  Output element (r, c)
+ * is written to
+ *   out[r * out_ld + c] = row_scale[r] * col_scale[c] * (H X H)[r][c]
  * with H the unnormalised 128-block +-1 Sylvester Hadamard (pass
  * row_scale = su / 128 to reproduce the normalised decode).
  */
@@ -111,6 +115,8 @@ typedef struct qsrt_decode_job {
     int64_t out_ld;
     int64_t rows;
     int64_t cols;
+    int64_t block_row_stride;
+    int64_t block_col_stride;
 } qsrt_decode_job;
 
 /* Device workspace bytes qsrt_decode needs for n_jobs jobs. */
@@ -122,16 +128,39 @@ size_t qsrt_decode_workspace_bytes(int n_jobs);
  *   words -> cyclic 16-bit states -> lut_e4m3[state] -> X (tensor-core
  *   order inside each 16x16 tile) -> row_scale . H128 X H128 . col_scale.
  * `jobs` is a HOST array (copied to `workspace` on `stream`); rows and cols
- * multiples of 128; words 4-byte aligned with even strides; out 8-byte
- * (bf16) / 16-byte (f32) aligned; out_ld % 4 == 0; col_scale 16-byte
- * aligned.  exact_fp8 != 0 selects the FP8 matrix-core path, exact for
- * LUTs with |label| <= 6 (every SQG table); 0 the FP32 path (any LUT).
+ * multiples of 128; words, out, row_scale and col_scale 16-byte aligned;
+ * tile and block strides multiples of 8; out_ld >= cols and a multiple of 8; lut_e4m3
+ * 16-byte aligned.  exact_fp8 != 0 selects the FP8 matrix-core path, exact
+ * for LUTs with |label| <= 6 (every SQG table); 0 the FP32 path (any LUT).
+ * Equivalent to qsrt_decode_prepare followed by qsrt_decode_execute.
  * Replaces decode_exl3_weight / decode_qsrt_weight
  * (qsrt/exl3_reference.py:61-330) and decode_qsrt_exl3_weight
  * (qsrt/qsrt.py:1175-1209).
  */
 int qsrt_decode(const qsrt_decode_job *jobs, int n_jobs, int K, const uint8_t *lut_e4m3, int exact_fp8,
                 int out_dtype, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * A validated job table resident in a caller's workspace: decode the same
+ * set of payloads many times (a serving layer, a benchmark) without
+ * re-validating or re-uploading it.  Plain data: copy it freely; it stays
+ * valid while the workspace and every pointer in the jobs do.
+ */
+typedef struct qsrt_decode_plan {
+    const void *jobs;     /* device job table inside the workspace */
+    int n_jobs;           /* non-empty jobs */
+    int K;
+    int64_t total_blocks; /* 128 x 128 blocks over all jobs */
+} qsrt_decode_plan;
+
+/* Validate `jobs` (same rules as qsrt_decode) and upload them into
+ * `workspace` on `stream`; fills *plan. */
+int qsrt_decode_prepare(const qsrt_decode_job *jobs, int n_jobs, int K, void *workspace, size_t workspace_bytes,
+                        qsrt_decode_plan *plan, void *stream);
+
+/* One launch over a prepared plan (stream-ordered after its upload). */
+int qsrt_decode_execute(const qsrt_decode_plan *plan, const uint8_t *lut_e4m3, int exact_fp8, int out_dtype,
+                        void *stream);
 
 /*
  * C[M, N] += alpha * A^T (B - B2) on the matrix cores, all row-major:

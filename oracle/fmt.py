@@ -93,7 +93,14 @@ def tiles_to_matrix(tile_values: np.ndarray) -> np.ndarray:
 def decode(states: np.ndarray, label_values: np.ndarray, suh: np.ndarray, svh: np.ndarray) -> np.ndarray:
     """float64 decode: labels -> [K, N] -> H_L -> *suh -> H_R -> *svh."""
 
-    x = tiles_to_matrix(label_values[np.asarray(states, dtype=np.int64) & 0xFFFF].astype(np.float64))
+    return decode_tile_values(label_values[np.asarray(states, dtype=np.int64) & 0xFFFF], suh, svh)
+
+
+def decode_tile_values(tile_values: np.ndarray, suh: np.ndarray, svh: np.ndarray) -> np.ndarray:
+    """float64 decode of per-tile label values ``[K/16, N/16, 256]`` (mixed
+    rates: each tile's labels looked up in its own rate's table)."""
+
+    x = tiles_to_matrix(np.asarray(tile_values, dtype=np.float64))
     k, n = x.shape
     h = hadamard(128)
     x = np.einsum("ij,bjn->bin", h, x.reshape(k // 128, 128, n)).reshape(k, n)

@@ -39,6 +39,8 @@ SIGNATURES: dict[str, tuple] = {
     "qsrt_unpack_states": (_c_int, [_c_void_p, _c_i64, _c_int, _c_void_p, _c_void_p]),
     "qsrt_decode_workspace_bytes": (_c_size, [_c_int]),
     "qsrt_decode": (_c_int, [_c_void_p, _c_int, _c_int, _c_void_p, _c_int, _c_int, _c_void_p, _c_size, _c_void_p]),
+    "qsrt_decode_prepare": (_c_int, [_c_void_p, _c_int, _c_int, _c_void_p, _c_size, _c_void_p, _c_void_p]),
+    "qsrt_decode_execute": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
     "qsrt_gemm_tn": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float,
@@ -64,6 +66,19 @@ class DecodeJob(ctypes.Structure):
         ("out_ld", _c_i64),
         ("rows", _c_i64),
         ("cols", _c_i64),
+        ("block_row_stride", _c_i64),
+        ("block_col_stride", _c_i64),
+    ]
+
+
+class DecodePlanStruct(ctypes.Structure):
+    """``qsrt_decode_plan`` of ``include/qsrt_amd.h``."""
+
+    _fields_ = [
+        ("jobs", _c_void_p),
+        ("n_jobs", _c_int),
+        ("K", _c_int),
+        ("total_blocks", _c_i64),
     ]
 
 

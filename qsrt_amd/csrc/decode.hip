@@ -66,6 +66,8 @@ struct Job {
     const int16_t* words;
     int64_t tile_row_stride;
     int64_t tile_col_stride;
+    int64_t block_row_stride;  // words between vertically adjacent 128 x 128 blocks
+    int64_t block_col_stride;  // words between horizontally adjacent blocks
     const float* row_scale;
     const float* col_scale;
     void* out;
@@ -111,7 +113,7 @@ struct BlockCtx {
 __device__ __forceinline__ BlockCtx block_ctx(const Job* jobs, const Cursor& cu, int out_size) {
     const Job& J = jobs[cu.j];
     BlockCtx x;
-    x.words = J.words + 8 * (cu.br * J.tile_row_stride + cu.bc * J.tile_col_stride);
+    x.words = J.words + cu.br * J.block_row_stride + cu.bc * J.block_col_stride;
     x.trs = J.tile_row_stride;
     x.tcs = J.tile_col_stride;
     x.su = J.row_scale + 128 * cu.br;
@@ -374,19 +376,19 @@ size_t qsrt_decode_workspace_bytes(int n_jobs) {
     return static_cast<size_t>(n_jobs) * sizeof(Job);
 }
 
-int qsrt_decode(const qsrt_decode_job* jobs, int n_jobs, int K, const uint8_t* lut_e4m3, int exact_fp8,
-                int out_dtype, void* workspace, size_t workspace_bytes, void* stream_handle) {
+int qsrt_decode_prepare(const qsrt_decode_job* jobs, int n_jobs, int K, void* workspace, size_t workspace_bytes,
+                        qsrt_decode_plan* plan, void* stream_handle) {
     hipStream_t stream = static_cast<hipStream_t>(stream_handle);
+    if (!plan) return qsrt::fail(qsrt::kBadArgument, "null plan pointer");
+    *plan = qsrt_decode_plan{workspace, 0, K, 0};
     if (K < 2 || K > 4) return qsrt::fail(qsrt::kBadArgument, "K%d decode is not supported (K2..K4)", K);
     if (n_jobs < 0) return qsrt::fail(qsrt::kBadArgument, "n_jobs must be non-negative");
-    if (out_dtype != 0 && out_dtype != 1) return qsrt::fail(qsrt::kBadArgument, "out_dtype must be 0 (bf16) or 1 (f32)");
     if (n_jobs == 0) return qsrt::kOk;
-    if (!jobs || !lut_e4m3 || !workspace) return qsrt::fail(qsrt::kBadArgument, "null pointer argument");
+    if (!jobs || !workspace) return qsrt::fail(qsrt::kBadArgument, "null pointer argument");
     if (workspace_bytes < qsrt_decode_workspace_bytes(n_jobs))
         return qsrt::fail(qsrt::kWorkspaceTooSmall, "decode workspace needs %zu bytes",
                           qsrt_decode_workspace_bytes(n_jobs));
-    if (reinterpret_cast<uintptr_t>(lut_e4m3) % 16 || reinterpret_cast<uintptr_t>(workspace) % 16)
-        return qsrt::fail(qsrt::kBadArgument, "LUT and workspace must be 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(workspace) % 16) return qsrt::fail(qsrt::kBadArgument, "workspace must be 16-byte aligned");
     Job* host = static_cast<Job*>(malloc(sizeof(Job) * n_jobs));
     if (!host) return qsrt::fail(qsrt::kHipError, "host allocation failed");
     int64_t total = 0;
@@ -394,17 +396,18 @@ int qsrt_decode(const qsrt_decode_job* jobs, int n_jobs, int K, const uint8_t* l
     for (int i = 0; i < n_jobs; ++i) {
         const qsrt_decode_job& s = jobs[i];
         const bool ok = s.words && s.row_scale && s.col_scale && s.out && s.rows >= 0 && s.cols >= 0 &&
-                        s.rows % 128 == 0 && s.cols % 128 == 0 && s.out_ld >= s.cols && s.out_ld % 4 == 0 &&
+                        s.rows % 128 == 0 && s.cols % 128 == 0 && s.out_ld >= s.cols && s.out_ld % 8 == 0 &&
                         reinterpret_cast<uintptr_t>(s.words) % 16 == 0 && s.tile_row_stride % 8 == 0 &&
-                        s.tile_col_stride % 8 == 0 && reinterpret_cast<uintptr_t>(s.out) % 16 == 0 &&
-                        s.out_ld % 8 == 0 &&
+                        s.tile_col_stride % 8 == 0 && s.block_row_stride % 8 == 0 && s.block_col_stride % 8 == 0 &&
+                        reinterpret_cast<uintptr_t>(s.out) % 16 == 0 &&
                         reinterpret_cast<uintptr_t>(s.col_scale) % 16 == 0 &&
                         reinterpret_cast<uintptr_t>(s.row_scale) % 16 == 0;
         if (!ok) {
             free(host);
             return qsrt::fail(qsrt::kBadArgument,
                               "decode job %d: need rows, cols multiples of 128, out_ld >= cols and a multiple of 8, "
-                              "16-byte aligned words, out, row_scale and col_scale, tile strides multiples of 8, non-null pointers",
+                              "16-byte aligned words, out, row_scale and col_scale, tile and block strides multiples of 8, "
+                              "non-null pointers",
                               i);
         }
         if (s.rows / 128 >= (1 << 30) || s.cols / 128 >= (1 << 30)) {
@@ -412,31 +415,63 @@ int qsrt_decode(const qsrt_decode_job* jobs, int n_jobs, int K, const uint8_t* l
             return qsrt::fail(qsrt::kBadArgument, "decode job %d is too large", i);
         }
         if (s.rows == 0 || s.cols == 0) continue;  // nothing to decode; the kernel never sees empty jobs
-        host[kept++] = Job{s.words, s.tile_row_stride, s.tile_col_stride, s.row_scale, s.col_scale, s.out, s.out_ld,
-                           static_cast<int32_t>(s.rows / 128), static_cast<int32_t>(s.cols / 128), total};
+        host[kept++] = Job{s.words,
+                           s.tile_row_stride,
+                           s.tile_col_stride,
+                           s.block_row_stride ? s.block_row_stride : 8 * s.tile_row_stride,
+                           s.block_col_stride ? s.block_col_stride : 8 * s.tile_col_stride,
+                           s.row_scale,
+                           s.col_scale,
+                           s.out,
+                           s.out_ld,
+                           static_cast<int32_t>(s.rows / 128),
+                           static_cast<int32_t>(s.cols / 128),
+                           total};
         total += (s.rows / 128) * (s.cols / 128);
     }
-    if (kept == 0) {
-        free(host);
-        return qsrt::kOk;
-    }
-    const hipError_t cp = hipMemcpyAsync(workspace, host, sizeof(Job) * kept, hipMemcpyHostToDevice, stream);
+    // pageable source: the call returns once the table is staged, so the host copy can go
+    const hipError_t cp =
+        kept ? hipMemcpyAsync(workspace, host, sizeof(Job) * kept, hipMemcpyHostToDevice, stream) : hipSuccess;
     free(host);
     if (cp != hipSuccess) return qsrt::fail(qsrt::kHipError, "job upload failed: %s", hipGetErrorString(cp));
-    if (total == 0) return qsrt::kOk;
+    *plan = qsrt_decode_plan{workspace, kept, K, total};
+    return qsrt::kOk;
+}
+
+int qsrt_decode_execute(const qsrt_decode_plan* plan, const uint8_t* lut_e4m3, int exact_fp8, int out_dtype,
+                        void* stream_handle) {
+    hipStream_t stream = static_cast<hipStream_t>(stream_handle);
+    if (!plan) return qsrt::fail(qsrt::kBadArgument, "null plan pointer");
+    if (out_dtype != 0 && out_dtype != 1) return qsrt::fail(qsrt::kBadArgument, "out_dtype must be 0 (bf16) or 1 (f32)");
+    if (plan->K < 2 || plan->K > 4) return qsrt::fail(qsrt::kBadArgument, "plan holds an unsupported K%d", plan->K);
+    if (plan->n_jobs < 0 || plan->total_blocks < 0) return qsrt::fail(qsrt::kBadArgument, "malformed decode plan");
+    if (plan->n_jobs == 0 || plan->total_blocks == 0) return qsrt::kOk;
+    if (!plan->jobs || !lut_e4m3) return qsrt::fail(qsrt::kBadArgument, "null pointer argument");
+    if (reinterpret_cast<uintptr_t>(lut_e4m3) % 16) return qsrt::fail(qsrt::kBadArgument, "LUT must be 16-byte aligned");
     int cus = 0;
     if (const int rc = qsrt::current_cu_count(&cus)) return rc;
-    const Job* dj = static_cast<const Job*>(workspace);
-    switch (K * 2 + (exact_fp8 ? 1 : 0)) {
-        case 5: launch<2, true>(dj, kept, total, lut_e4m3, out_dtype, cus, stream); break;
-        case 4: launch<2, false>(dj, kept, total, lut_e4m3, out_dtype, cus, stream); break;
-        case 7: launch<3, true>(dj, kept, total, lut_e4m3, out_dtype, cus, stream); break;
-        case 6: launch<3, false>(dj, kept, total, lut_e4m3, out_dtype, cus, stream); break;
-        case 9: launch<4, true>(dj, kept, total, lut_e4m3, out_dtype, cus, stream); break;
-        default: launch<4, false>(dj, kept, total, lut_e4m3, out_dtype, cus, stream); break;
+    const Job* dj = static_cast<const Job*>(plan->jobs);
+    const int n = plan->n_jobs;
+    const int64_t total = plan->total_blocks;
+    switch (plan->K * 2 + (exact_fp8 ? 1 : 0)) {
+        case 5: launch<2, true>(dj, n, total, lut_e4m3, out_dtype, cus, stream); break;
+        case 4: launch<2, false>(dj, n, total, lut_e4m3, out_dtype, cus, stream); break;
+        case 7: launch<3, true>(dj, n, total, lut_e4m3, out_dtype, cus, stream); break;
+        case 6: launch<3, false>(dj, n, total, lut_e4m3, out_dtype, cus, stream); break;
+        case 9: launch<4, true>(dj, n, total, lut_e4m3, out_dtype, cus, stream); break;
+        default: launch<4, false>(dj, n, total, lut_e4m3, out_dtype, cus, stream); break;
     }
     QSRT_HIP_TRY(hipGetLastError());
     return qsrt::kOk;
+}
+
+int qsrt_decode(const qsrt_decode_job* jobs, int n_jobs, int K, const uint8_t* lut_e4m3, int exact_fp8,
+                int out_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+    if (out_dtype != 0 && out_dtype != 1) return qsrt::fail(qsrt::kBadArgument, "out_dtype must be 0 (bf16) or 1 (f32)");
+    if (n_jobs > 0 && !lut_e4m3) return qsrt::fail(qsrt::kBadArgument, "null pointer argument");
+    qsrt_decode_plan plan;
+    if (const int rc = qsrt_decode_prepare(jobs, n_jobs, K, workspace, workspace_bytes, &plan, stream)) return rc;
+    return qsrt_decode_execute(&plan, lut_e4m3, exact_fp8, out_dtype, stream);
 }
 
 }  // extern "C"

@@ -78,17 +78,55 @@ def decode_words(words: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor, bits
     elif out.shape != (k, n) or out.dtype != out_dtype or out.stride(1) != 1:
         raise ValueError("out must be a row-major [K, N] tensor of out_dtype")
     job = _native.DecodeJob(words.data_ptr(), nt * 16 * bits, 16 * bits, su.data_ptr(), sv.data_ptr(),
-                            out.data_ptr(), out.stride(0), k, n)
+                            out.data_ptr(), out.stride(0), k, n, 0, 0)
     _run([job], bits, lut, out_dtype, dev)
     return out
+
+
+def record_jobs(words_ptr: int, record_bits, rate_axis: str, k: int, n: int, su: torch.Tensor, sv: torch.Tensor,
+                out: torch.Tensor) -> tuple[dict[int, list], int]:
+    """Decode jobs of one record-major payload (``pack_qsrt_trellis`` layout:
+    records of 128 rate-axis channels, each ``[tiles, 16 K]`` words in
+    row-major tile order), grouped by rate.  A run of consecutive same-rate
+    records is one job: along K the run is a contiguous row strip, along N its
+    records are the block columns (one record apart in the payload).
+    Returns the jobs by rate and the number of int16 words the records use."""
+
+    from .qsrt import TILE_CHANNELS, TILES_PER_RECORD_AXIS
+
+    esize = out.element_size()
+    kt, nt = k // TILE_CHANNELS, n // TILE_CHANNELS
+    other = nt if rate_axis == "k" else kt
+    runs = []  # [bits, first record, word offset, records]
+    cursor = 0
+    for record, bits in enumerate(record_bits):
+        if runs and runs[-1][0] == bits:
+            runs[-1][3] += 1
+        else:
+            runs.append([bits, record, cursor, 1])
+        cursor += TILES_PER_RECORD_AXIS * other * 16 * bits
+    by_bits: dict[int, list] = {}
+    for bits, first, offset, count in runs:
+        r0 = first * TILES_PER_RECORD_AXIS * TILE_CHANNELS
+        wpt = 16 * bits
+        if rate_axis == "k":
+            job = _native.DecodeJob(words_ptr + 2 * offset, nt * wpt, wpt, su.data_ptr() + 4 * r0, sv.data_ptr(),
+                                    out.data_ptr() + esize * r0 * out.stride(0), out.stride(0), 128 * count, n, 0, 0)
+        else:
+            job = _native.DecodeJob(words_ptr + 2 * offset, TILES_PER_RECORD_AXIS * wpt, wpt, su.data_ptr(),
+                                    sv.data_ptr() + 4 * r0, out.data_ptr() + esize * r0, out.stride(0), k,
+                                    128 * count, 8 * TILES_PER_RECORD_AXIS * wpt, TILES_PER_RECORD_AXIS * kt * wpt)
+        by_bits.setdefault(bits, []).append(job)
+    return by_bits, cursor
 
 
 def decode_packed(packed, suh: torch.Tensor, svh: torch.Tensor, luts_by_bits: dict, *, out_dtype=torch.bfloat16,
                   out: torch.Tensor | None = None) -> torch.Tensor:
     """Mixed-rate ``PackedQSRTTrellis`` -> ``[K, N]`` weights: every 128-channel
-    record along the rate axis is one decode job at its own rate."""
+    record along the rate axis is decoded at its own rate (one launch per
+    rate)."""
 
-    from .qsrt import TILE_CHANNELS, TILES_PER_RECORD_AXIS, record_bits
+    from .qsrt import TILE_CHANNELS, record_bits
 
     packed.validate()
     d = packed.descriptor
@@ -103,21 +141,8 @@ def decode_packed(packed, suh: torch.Tensor, svh: torch.Tensor, luts_by_bits: di
         out = torch.empty((k, n), dtype=out_dtype, device=dev)
     elif out.shape != (k, n) or out.dtype != out_dtype or out.stride(1) != 1:
         raise ValueError("out must be a row-major [K, N] tensor of out_dtype")
-    esize = out.element_size()
-    by_bits: dict[int, list] = {}
-    cursor = 0
-    base = payload.data_ptr()
-    for record, bits in enumerate(record_bits(d.mode)):
-        r0 = record * TILES_PER_RECORD_AXIS * TILE_CHANNELS
-        if d.rate_axis == "k":
-            job = _native.DecodeJob(base + 2 * cursor, d.n_tiles * 16 * bits, 16 * bits, su.data_ptr() + 4 * r0,
-                                    sv.data_ptr(), out.data_ptr() + esize * r0 * out.stride(0), out.stride(0), 128, n)
-        else:
-            job = _native.DecodeJob(base + 2 * cursor, TILES_PER_RECORD_AXIS * 16 * bits, 16 * bits, su.data_ptr(),
-                                    sv.data_ptr() + 4 * r0, out.data_ptr() + esize * r0, out.stride(0), k, 128)
-        by_bits.setdefault(bits, []).append(job)
-        cursor += d.tiles_per_record * 16 * bits
-    if cursor != payload.numel():
+    by_bits, used = record_jobs(payload.data_ptr(), record_bits(d.mode), d.rate_axis, k, n, su, sv, out)
+    if used != payload.numel():
         raise ValueError("QSRT trellis payload has trailing data")
     for bits, jobs in sorted(by_bits.items()):
         _run(jobs, bits, _check_lut(luts_by_bits[bits], dev), out_dtype, dev)
@@ -125,37 +150,69 @@ def decode_packed(packed, suh: torch.Tensor, svh: torch.Tensor, luts_by_bits: di
 
 
 class DecodePlan:
-    """A fixed set of uniform-rate matrices decoded by one launch.
+    """A fixed set of payloads decoded again and again: the job table of each
+    rate is validated and uploaded once (``qsrt_decode_prepare``) and
+    ``run()`` is one launch per rate (``qsrt_decode_execute``).
 
     ``matrices`` is a list of ``(words [K/16, N/16, 16 bits], su f32 [K] (already
-    divided by 128), sv f32 [N], out [K, N])`` on one device; the job table is
-    built once, so ``run()`` only uploads it and launches."""
+    divided by 128), sv f32 [N], out [K, N])`` at the uniform rate ``bits``;
+    :meth:`for_records` builds a plan over mixed-rate record-major payloads."""
 
-    def __init__(self, matrices: list, bits: int, lut: torch.Tensor, *, out_dtype=torch.bfloat16):
-        if not matrices:
-            raise ValueError("empty decode plan")
-        dev = matrices[0][0].device
-        self.bits, self.device, self.out_dtype = bits, dev, out_dtype
-        self.lut = _check_lut(lut, dev)
-        self._keep = matrices
-        jobs = []
-        for words, su, sv, out in matrices:
-            kt, nt, wpt = words.shape
-            if wpt != 16 * bits or out.shape != (16 * kt, 16 * nt) or out.dtype != out_dtype:
-                raise ValueError("decode plan entry does not match its output")
-            jobs.append(_native.DecodeJob(words.data_ptr(), nt * 16 * bits, 16 * bits, su.data_ptr(), sv.data_ptr(),
-                                          out.data_ptr(), out.stride(0), 16 * kt, 16 * nt))
-        self._arr = (_native.DecodeJob * len(jobs))(*jobs)
-        self._n = len(jobs)
+    def __init__(self, matrices: list | None, bits: int | None, lut: torch.Tensor | None, *, out_dtype=torch.bfloat16,
+                 _jobs_by_bits: dict | None = None, _luts: dict | None = None, _device=None, _keep=None):
+        if _jobs_by_bits is None:
+            if not matrices:
+                raise ValueError("empty decode plan")
+            jobs = []
+            for words, su, sv, out in matrices:
+                kt, nt, wpt = words.shape
+                if wpt != 16 * bits or out.shape != (16 * kt, 16 * nt) or out.dtype != out_dtype:
+                    raise ValueError("decode plan entry does not match its output")
+                jobs.append(_native.DecodeJob(words.data_ptr(), nt * 16 * bits, 16 * bits, su.data_ptr(),
+                                              sv.data_ptr(), out.data_ptr(), out.stride(0), 16 * kt, 16 * nt, 0, 0))
+            _jobs_by_bits = {bits: jobs}
+            _device = matrices[0][0].device
+            _luts = {bits: lut}
+            _keep = matrices
+        if out_dtype not in _OUT:
+            raise ValueError("out_dtype must be torch.bfloat16 or torch.float32")
+        self.device, self.out_dtype, self._keep = _device, out_dtype, _keep
         lib = _native.lib()
-        self._ws = torch.empty(max(int(lib.qsrt_decode_workspace_bytes(self._n)), 16), dtype=torch.uint8, device=dev)
-        self._fp8 = int(_lut_abs_max(self.lut) <= FP8_EXACT_MAX_LABEL)
+        stream = _native.stream_handle(_device)
+        self._plans = []
+        for bits, jobs in sorted(_jobs_by_bits.items()):
+            lut = _check_lut(_luts[bits], _device)
+            arr = (_native.DecodeJob * len(jobs))(*jobs)
+            ws = torch.empty(max(int(lib.qsrt_decode_workspace_bytes(len(jobs))), 16), dtype=torch.uint8,
+                             device=_device)
+            plan = _native.DecodePlanStruct()
+            _native.check(lib.qsrt_decode_prepare(ctypes.cast(arr, ctypes.c_void_p), len(jobs), bits, ws.data_ptr(),
+                                                  ws.numel(), ctypes.byref(plan), stream), "qsrt_decode_prepare")
+            self._plans.append((plan, lut, ws, int(_lut_abs_max(lut) <= FP8_EXACT_MAX_LABEL)))
+
+    @classmethod
+    def for_records(cls, payloads: list, luts_by_bits: dict, *, out_dtype=torch.bfloat16) -> "DecodePlan":
+        """``payloads``: ``(words int16 (flat, record-major), record_bits, rate_axis, su f32 [K] / 128,
+        sv f32 [N], out [K, N])`` tuples."""
+
+        if not payloads:
+            raise ValueError("empty decode plan")
+        merged: dict[int, list] = {}
+        for words, rbits, axis, su, sv, out in payloads:
+            if out.dtype != out_dtype or out.stride(1) != 1:
+                raise ValueError("decode plan outputs must be row-major tensors of out_dtype")
+            k, n = out.shape
+            jobs, used = record_jobs(words.data_ptr(), tuple(rbits), axis, k, n, su, sv, out)
+            if used != words.numel():
+                raise ValueError("record payload length does not match its rates")
+            for bits, js in jobs.items():
+                merged.setdefault(bits, []).extend(js)
+        return cls(None, None, None, out_dtype=out_dtype, _jobs_by_bits=merged,
+                   _luts={b: luts_by_bits[b] for b in merged}, _device=payloads[0][0].device, _keep=payloads)
 
     def run(self) -> None:
         lib = _native.lib()
-        _native.check(
-            lib.qsrt_decode(ctypes.cast(self._arr, ctypes.c_void_p), self._n, self.bits, self.lut.data_ptr(),
-                            self._fp8, _OUT[self.out_dtype], self._ws.data_ptr(), self._ws.numel(),
-                            _native.stream_handle(self.device)),
-            "qsrt_decode",
-        )
+        stream = _native.stream_handle(self.device)
+        for plan, lut, _ws, fp8 in self._plans:
+            _native.check(lib.qsrt_decode_execute(ctypes.byref(plan), lut.data_ptr(), fp8, _OUT[self.out_dtype],
+                                                  stream), "qsrt_decode_execute")

@@ -108,6 +108,78 @@ def test_decode_mixed_rate_payload(rate_axis):
     assert np.max(np.abs(got.cpu().double().numpy() - want)) <= 2e-6 * np.abs(want).max()
 
 
+def _record_payload(rbits, rate_axis, other_tiles, seed):
+    """Record-major words of random closed paths, one record (8 rate-axis
+    tiles) per rate in ``rbits``; returns (states [kt, nt, 256], words)."""
+
+    g = torch.Generator().manual_seed(seed)
+    r = len(rbits)
+    shape = (8 * r, other_tiles) if rate_axis == "k" else (other_tiles, 8 * r)
+    states = torch.empty((*shape, 256), dtype=torch.int16)
+    pieces = []
+    for i, bits in enumerate(rbits):
+        e = torch.randint(0, 1 << bits, (8, other_tiles, 256) if rate_axis == "k" else (other_tiles, 8, 256),
+                          generator=g)
+        st = reconstruct_trellis_states(e, bits)
+        if rate_axis == "k":
+            states[8 * i:8 * i + 8] = st
+        else:
+            states[:, 8 * i:8 * i + 8] = st
+        pieces.append(Q.pack_trellis_edges(st.reshape(-1, 256), bits).reshape(-1))
+    return states, torch.cat(pieces)
+
+
+def test_decode_plan_over_mixed_records_matches_the_oracle():
+    """Prepared plan over two record-major payloads (records along K with
+    mergeable same-rate runs, records along N), run twice; the oracle looks
+    every tile's labels up in its own record's table."""
+
+    _say("[decode] prepared plan over mixed-rate records")
+    cases = [((3, 3, 4, 4, 3), "k", 16, 41), ((2, 4, 3, 3), "n", 8, 42)]
+    luts = {b: sqg_xor_cheb_t12_bytes(b).cuda() for b in (2, 3, 4)}
+    payloads, wants = [], []
+    for rbits, axis, other, seed in cases:
+        states, words = _record_payload(rbits, axis, other, seed)
+        kt, nt = states.shape[:2]
+        g = torch.Generator().manual_seed(seed + 100)
+        suh = (torch.rand(16 * kt, generator=g) + 0.5).half()
+        svh = (torch.rand(16 * nt, generator=g) - 0.5).half()
+        st = states.numpy().view(np.uint16)
+        labels = np.empty((kt, nt, 256), dtype=np.float64)
+        for i, bits in enumerate(rbits):
+            sl = (slice(8 * i, 8 * i + 8), slice(None)) if axis == "k" else (slice(None), slice(8 * i, 8 * i + 8))
+            labels[sl] = otables.t12_values(bits)[st[sl]]
+        wants.append(ofmt.decode_tile_values(labels, suh.float().numpy(), svh.float().numpy()))
+        out = torch.empty((16 * kt, 16 * nt), dtype=torch.float32, device="cuda")
+        payloads.append((words.cuda(), rbits, axis, (suh.float() / 128).cuda(), svh.float().cuda(), out))
+    plan = D.DecodePlan.for_records(payloads, luts, out_dtype=torch.float32)
+    plan.run()
+    first = [p[5].clone() for p in payloads]
+    plan.run()
+    for want, p, f in zip(wants, payloads, first):
+        assert torch.equal(p[5], f)
+        assert np.max(np.abs(p[5].cpu().double().numpy() - want)) <= 2e-6 * np.abs(want).max()
+
+
+def test_decode_plan_api_edges():
+    from qsrt_amd import _native
+    import ctypes
+    lib = _native.lib()
+    plan = _native.DecodePlanStruct()
+    ws = torch.empty(16, dtype=torch.uint8, device="cuda")
+    _native.check(lib.qsrt_decode_prepare(None, 0, 3, ws.data_ptr(), ws.numel(), ctypes.byref(plan),
+                                          _native.stream_handle(ws.device)), "prepare")
+    assert plan.n_jobs == 0 and plan.total_blocks == 0
+    lut = sqg_xor_cheb_t12_bytes(3).cuda()
+    _native.check(lib.qsrt_decode_execute(ctypes.byref(plan), lut.data_ptr(), 1, 0, _native.stream_handle(ws.device)),
+                  "execute")
+    plan.K = 7
+    plan.n_jobs = 1
+    plan.total_blocks = 1
+    assert lib.qsrt_decode_execute(ctypes.byref(plan), lut.data_ptr(), 1, 0, _native.stream_handle(ws.device)) != 0
+    assert b"K7" in lib.qsrt_last_error()
+
+
 def test_decode_into_strided_output_leaves_the_rest():
     bits = 2
     states, suh, svh = _payload(bits, 8, 8, 21)
