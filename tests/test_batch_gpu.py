@@ -115,3 +115,61 @@ def test_quantize_qsrt_batch_candidates_close_and_decode():
                 assert float((dec - res["weight_q"]).abs().max()) <= 1e-5 * float(res["weight_q"].abs().max())
     with pytest.raises(ValueError):
         be.quantize_qsrt_batch(weights, H_datas, [groups[0], []])
+
+
+def _direct(W, L, qas_by_source):
+    """Every (source, candidate) encoded on its own, source-major."""
+
+    out_q, out_e = [], []
+    for s, qas in enumerate(qas_by_source):
+        for qa in qas:
+            q, e = be.ldlq_mixed(W[s], L[s], qa)
+            out_q.append(q)
+            out_e.append(e)
+    return torch.stack(out_q), torch.stack(out_e)
+
+
+def test_output_axis_candidate_reuse_is_bit_identical():
+    """R0/R1/R2-style ladders along N: one all-K3 encode plus the union of
+    replacement tiles per width reproduces every candidate exactly."""
+
+    print("[batch] ldlq_mixed_n_candidates_reuse", file=sys.stderr, flush=True)
+    k, n = 256, 512
+    W0, L0, _ = _problem(k, n, 11)
+    W1, L1, _ = _problem(k, n, 12)
+    t = n // 16
+    r1 = [2] * 8 + [3] * (t - 16) + [4] * 8
+    r2 = [2] * 16 + [3] * (t - 32) + [4] * 16
+    groups = [[_qa([3] * t), _qa(r1), _qa(r2)], [_qa([3] * t), _qa(r2)]]
+    W, L = torch.stack([W0, W1]), torch.stack([L0, L1])
+    q, e = be.ldlq_mixed_n_candidates_reuse(W, L, groups)
+    dq, de = _direct(W, L, groups)
+    assert torch.equal(q, dq) and torch.equal(e, de)
+    with pytest.raises(ValueError, match="all-K3"):
+        be.ldlq_mixed_n_candidates_reuse(W, L, [[_qa(r1)], [_qa(r2)]])
+    with pytest.raises(ValueError, match="multiple non-K3"):
+        be.ldlq_mixed_n_candidates_reuse(W[:1], L[:1], [[_qa([3] * t), _qa([2] * t), _qa([4] * t)]])
+
+
+def test_input_axis_prefix_reuse_is_bit_identical():
+    """Candidates along K that agree on the last records: the shared suffix is
+    encoded once and the trie continues only where the maps differ."""
+
+    print("[batch] ldlq_mixed_k_candidates_prefix_reuse", file=sys.stderr, flush=True)
+    k, n = 512, 256
+    W0, L0, _ = _problem(k, n, 21)
+    W1, L1, _ = _problem(k, n, 22)
+    t = k // 16
+    base = [3] * t
+    a = [2] * 8 + [4] * 8 + [3] * (t - 16)          # differs in the first two 128-row spans
+    b = [2] * 8 + [3] * 8 + [4] * 8 + [3] * (t - 24)  # shares span 0 with a, differs in span 1 and 2
+    groups = [[_qa(base, "k"), _qa(a, "k"), _qa(b, "k")], [_qa(a, "k"), _qa(b, "k")]]
+    W, L = torch.stack([W0, W1]), torch.stack([L0, L1])
+    q, e = be.ldlq_mixed_k_candidates_prefix_reuse(W, L, groups)
+    dq, de = _direct(W, L, groups)
+    assert torch.equal(q, dq) and torch.equal(e, de)
+    # no shared suffix at all: the flat batch
+    c = [4] * 8 + [3] * (t - 16) + [2] * 8
+    q, e = be.ldlq_mixed_k_candidates_prefix_reuse(W[:1], L[:1], [[_qa(base, "k"), _qa(c, "k")]])
+    dq, de = _direct(W[:1], L[:1], [[_qa(base, "k"), _qa(c, "k")]])
+    assert torch.equal(q, dq) and torch.equal(e, de)
