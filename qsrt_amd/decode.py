@@ -15,7 +15,7 @@ import ctypes
 import torch
 
 from . import _native
-from .sqg_quantizer import _lut_abs_max
+from .sqg_quantizer import _lut_abs_max, _lut_on
 
 # FP8 matrix-core products are exact for labels up to this magnitude (every
 # SQG table: |label| <= 5.5); larger tables use the FP32 path.
@@ -26,7 +26,7 @@ _OUT = {torch.bfloat16: 0, torch.float32: 1}
 def _check_lut(lut: torch.Tensor, device) -> torch.Tensor:
     if lut.dtype != torch.uint8 or lut.numel() != 1 << 16:
         raise ValueError("decode LUT must be uint8[65536] E4M3 bytes")
-    lut = lut.reshape(-1).to(device).contiguous()
+    lut = _lut_on(lut.reshape(-1), torch.device(device))
     if lut.data_ptr() % 16:
         lut = lut.clone()
     return lut

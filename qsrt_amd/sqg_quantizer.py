@@ -37,7 +37,6 @@ from .sqg_e4m3 import sqg_e4m3_bytes
 K2_FAST_MAX_LABEL = 16.0
 
 _workspaces: dict[int, torch.Tensor] = {}
-_lut_abs_max_cache: dict[tuple, float] = {}
 
 
 def _workspace(device: torch.device, bits: int, n_tiles: int) -> torch.Tensor:
@@ -57,12 +56,33 @@ def _workspace(device: torch.device, bits: int, n_tiles: int) -> torch.Tensor:
 
 
 def _lut_abs_max(lut: torch.Tensor) -> float:
-    key = (str(lut.device), lut.data_ptr(), lut._version)
-    value = _lut_abs_max_cache.get(key)
-    if value is None:
-        value = float(lut.view(torch.float8_e4m3fn).to(torch.float32).abs().amax())
-        _lut_abs_max_cache[key] = value
+    """Largest label magnitude of an E4M3 LUT, remembered on the tensor
+    object itself (with its version counter) so that neither a reused device
+    address nor an in-place edit can return another table's value."""
+
+    hit = getattr(lut, "_qsrt_abs_max", None)
+    if hit is not None and hit[0] == lut._version:
+        return hit[1]
+    value = float(lut.view(torch.float8_e4m3fn).to(torch.float32).abs().amax())
+    lut._qsrt_abs_max = (lut._version, value)
     return value
+
+
+def _lut_on(lut: torch.Tensor, device: torch.device) -> torch.Tensor:
+    """``lut`` as a contiguous uint8 tensor on ``device``; the device copy of a
+    host table is made once per source tensor and version."""
+
+    if lut.device == device and lut.dtype == torch.uint8 and lut.is_contiguous():
+        return lut
+    copies = getattr(lut, "_qsrt_device_copies", None)
+    if copies is None:
+        copies = {}
+        lut._qsrt_device_copies = copies
+    hit = copies.get(str(device))
+    if hit is None or hit[0] != lut._version:
+        hit = (lut._version, lut.to(device=device, dtype=torch.uint8).contiguous())
+        copies[str(device)] = hit
+    return hit[1]
 
 
 def boundary_lag(bits: int, lut_abs_max: float, policy: str = "reference") -> int:
@@ -169,7 +189,7 @@ def _resolve_codebook(quant_args: dict, bits: int, device: torch.device) -> torc
         if codebook is None:
             codebook = sqg_e4m3_bytes(bits, mode, device=device)
             _R44_LUTS[key] = codebook
-    return codebook.to(device=device, dtype=torch.uint8).contiguous()
+    return _lut_on(codebook, device)
 
 
 def has_sqg_codebook(quant_args: dict) -> bool:

@@ -110,3 +110,21 @@ def test_oracle_e4m3_encoder_agrees_with_torch_and_round_trips():
     # ties to even at a midpoint between 1.0 (0x38) and 1.125 (0x39)
     assert otables.e4m3_encode(np.array([1.0625]))[0] == 0x38
     assert otables.e4m3_encode(np.array([1.1875]))[0] == 0x3A
+
+
+def test_lut_abs_max_is_per_tensor_and_version():
+    """The cached largest label belongs to one tensor object and version:
+    another table (even one that reuses a freed address) or an in-place edit
+    never sees a stale value (a stale 5.5 would route a wide table to the
+    FP8 decode path)."""
+
+    from qsrt_amd.sqg_quantizer import _lut_abs_max, _lut_on
+
+    a = sqg.sqg_xor_cheb_t12_bytes(3).clone()
+    b = a.clone()
+    assert _lut_abs_max(a) == 5.5
+    b[7] = 0x77  # E4M3 240
+    assert _lut_abs_max(b) == 240.0 and _lut_abs_max(a) == 5.5
+    a[9] = 0xF7  # -240, in place
+    assert _lut_abs_max(a) == 240.0
+    assert _lut_on(a, torch.device("cpu")) is a
