@@ -160,6 +160,119 @@ def run_expert_encode(bits: int = 3, hidden: int = 7168, inter: int = 2048, toke
     return out
 
 
+LAYER_EXPERTS = 384
+LAYER_TOKENS = 65536
+LAYER_ZIPF_S = 1.1
+
+
+def zipf_token_counts(experts: int = LAYER_EXPERTS, tokens: int = LAYER_TOKENS, s: float = LAYER_ZIPF_S,
+                      seed: int = 20261201 + 8) -> list[int]:
+    """Routed calibration tokens per expert: c_r proportional to r^-s over the
+    ranks, scaled to ``tokens`` with largest-remainder rounding, ranks mapped
+    to experts by a seeded permutation."""
+
+    w = [r ** -s for r in range(1, experts + 1)]
+    total = sum(w)
+    exact = [tokens * x / total for x in w]
+    counts = [int(math.floor(x)) for x in exact]
+    for i in sorted(range(experts), key=lambda i: exact[i] - counts[i], reverse=True)[:tokens - sum(counts)]:
+        counts[i] += 1
+    perm = torch.randperm(experts, generator=torch.Generator().manual_seed(seed)).tolist()
+    by_expert = [0] * experts
+    for rank, expert in enumerate(perm):
+        by_expert[expert] = counts[rank]
+    return by_expert
+
+
+def layer_encode_bench(sample: int = 8, batch: int = 8, rho: float = 0.85):
+    """BASELINE config 5 encode: ``sample`` experts of the 384-expert layer,
+    ``batch`` experts per encoder batch (their gate/up traversals share tile
+    launches, then their down traversals), mixed record rates (14 K3 + 2 K4
+    records per matrix, the decode line's schedule), exact coupled basis,
+    H13 from each expert's Zipf-routed tokens (captured before the timed
+    region), H2 rebuilt in the timed region from the reconstructed SwiGLU
+    activations.  The layer time is the sample's time scaled to 384 experts."""
+
+    from types import SimpleNamespace
+
+    from qsrt_amd import exl3_encoder_backend as be
+    from qsrt_amd import gemm
+    from qsrt_amd.ldlq import make_shared_h
+    from qsrt_amd.qsrt_coupled import CoupledHadamardSpec, coupled_execution, decode_coupled_weights, encode_coupled_weights
+    from qsrt_amd.qsrt_encoder import _qsrt_quant_args
+    from qsrt_amd.transform_seeds import default_qsrt_transform_seeds
+
+    dev = torch.device("cuda:0")
+    hidden, inter = 7168, 2048
+    counts = zipf_token_counts()
+    # experts spread over the routing ranks (every expert of the sample has tokens)
+    order = sorted(range(LAYER_EXPERTS), key=lambda e: -counts[e])
+    chosen = [order[int(i * (LAYER_EXPERTS - 1) / max(sample - 1, 1))] for i in range(sample)]
+    chosen = [e if counts[e] > 0 else order[0] for e in chosen]
+    rate_map = tuple(b for b in DECODE_RECORD_BITS for _ in range(8))  # per 16-channel tile of the rate axis
+    spec = CoupledHadamardSpec()
+    gen = torch.Generator().manual_seed(20261201 + 9)
+    experts = []
+    for e in chosen:
+        w = [student_t(shape, nu=5, std=0.015, gen=gen).bfloat16().float().to(dev)
+             for shape in ((inter, hidden), (inter, hidden), (hidden, inter))]
+        x = ar1_rows(max(counts[e], 1), hidden, rho, gen, dev)
+        g_c, u_c, d_c = encode_coupled_weights(tuple(w), spec)
+        ex = coupled_execution((g_c, u_c, d_c), spec)
+        h13 = ex.transform_h13(gemm.gram_(torch.zeros((hidden, hidden), device=dev), x, 1.0 / x.shape[0]))
+        experts.append({"expert": e, "tokens": x.shape[0], "x": x, "c": (g_c, u_c, d_c), "ex": ex, "h13": h13})
+    torch.cuda.synchronize()
+
+    def qa(matrix, axis, scope):
+        plan = SimpleNamespace(rate_axis=axis, encoder_tile_bits=rate_map)
+        return _qsrt_quant_args(plan, matrix=matrix, layer=24, device=dev, shared_scale_scope=scope,
+                                transform_seeds=default_qsrt_transform_seeds(24, matrix))
+
+    proxies = []
+    t0 = time.perf_counter()
+    for g0 in range(0, sample, batch):
+        group = experts[g0:g0 + batch]
+        weights, hs, qas = [], [], []
+        for item in group:
+            g_c, u_c, _ = item["c"]
+            for name, m in (("w1", g_c), ("w3", u_c)):
+                shared = make_shared_h(hidden, dev, item["h13"])
+                shared["count"] = item["tokens"]
+                weights.append(m.T.contiguous())
+                hs.append(shared)
+                qas.append([qa(name, "n", ("layer-bench", g0))])
+        up = be.quantize_qsrt_batch(weights, hs, qas)
+        weights, hs, qas = [], [], []
+        for i, item in enumerate(group):
+            g_c, u_c, d_c = item["c"]
+            g_hat, u_hat = up[2 * i][0]["weight_q"].T, up[2 * i + 1][0]["weight_q"].T
+            gs, us, _ = decode_coupled_weights((g_hat, u_hat, d_c), spec)
+            x = item["x"]
+            h = (torch.nn.functional.silu(x @ gs.T) * (x @ us.T)).contiguous()
+            h2 = item["ex"].transform_h2(gemm.gram_(torch.zeros((inter, inter), device=dev), h, 1.0 / x.shape[0]))
+            shared = make_shared_h(inter, dev, h2)
+            shared["count"] = item["tokens"]
+            weights.append(d_c.T.contiguous())
+            hs.append(shared)
+            qas.append([qa("w2", "k", ("layer-bench", g0))])
+        down = be.quantize_qsrt_batch(weights, hs, qas)
+        proxies += [r[0]["proxy"] for r in up] + [r[0]["proxy"] for r in down]
+    torch.cuda.synchronize()
+    seconds = time.perf_counter() - t0
+    weights_per_expert = 3 * hidden * inter
+    return {
+        "workload": f"config 5 layer encode: {sample} of {LAYER_EXPERTS} Kimi-class experts (Zipf s={LAYER_ZIPF_S} over "
+                    f"{LAYER_TOKENS} routed tokens), {batch} experts per batch, records 14 K3 + 2 K4, coupled basis, "
+                    f"LDLQ, H2 from reconstructed activations",
+        "sample_experts": chosen,
+        "sample_tokens": [item["tokens"] for item in experts],
+        "sample_seconds": round(seconds, 3),
+        "M_weights_per_s": round(sample * weights_per_expert / seconds / 1e6, 2),
+        "layer_seconds_extrapolated": round(seconds * LAYER_EXPERTS / sample, 1),
+        "proxy_err_mean": round(sum(proxies) / len(proxies), 5),
+    }
+
+
 def cpu_baseline(tiles_np, seconds_target: float = 12.0):
     """Time the oracle on a bounded sample (first tiles), K2 and K3."""
 
@@ -408,6 +521,8 @@ def main() -> int:
     ap.add_argument("--no-expert", action="store_true", help="skip the config-4 expert encode")
     ap.add_argument("--no-decode", action="store_true", help="skip the layer decode")
     ap.add_argument("--no-kernels", action="store_true", help="skip the GEMM and Hadamard kernel lines")
+    ap.add_argument("--no-layer", action="store_true", help="skip the config-5 layer encode sample")
+    ap.add_argument("--layer-sample", type=int, default=8, help="experts encoded for the config-5 layer estimate")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a device copy of BYTES (reference for HBM byte counters)")
     args = ap.parse_args()
@@ -522,6 +637,11 @@ def main() -> int:
         log("[bench] config-4 expert encode (K3)")
         result["expert_encode"] = expert_bench()
         log(f"[bench] expert {result['expert_encode']['seconds']} s, {result['expert_encode']['speedup_vs_cpu']}x CPU")
+    if not args.no_layer:
+        log("[bench] config-5 layer encode sample")
+        result["layer_encode"] = layer_encode_bench(sample=args.layer_sample)
+        log(f"[bench] layer sample {result['layer_encode']['sample_seconds']} s, "
+            f"{result['layer_encode']['M_weights_per_s']} M w/s, layer ~{result['layer_encode']['layer_seconds_extrapolated']} s")
     print(json.dumps(result), flush=True)
     return 0
 
