@@ -33,6 +33,24 @@ def situ(gate: Tensor, up: Tensor, *, beta: float = 4.0, linear_beta: float = 25
     return (gate_value * up_value).to(gate.dtype)
 
 
+def situ_derivatives(gate: Tensor, up: Tensor, *, beta: float = 4.0, linear_beta: float = 25.0) -> tuple[Tensor, Tensor]:
+    """Partial derivatives of :func:`situ` with respect to gate and up, each
+    carrying the other factor (reference ``qsrt/coupled_expert_study.py:162-179``).
+
+    With ``f(g) = beta tanh(g / beta) s(g)`` (``s`` the logistic) and
+    ``h(u) = linear_beta tanh(u / linear_beta)``: ``d/dg = h f'`` where
+    ``f' = (1 - tanh^2) s + beta tanh s (1 - s)``, and ``d/du = f (1 - tanh^2(u / linear_beta))``.
+    """
+
+    g, u = gate.float(), up.float()
+    t_g = torch.tanh(g / beta)
+    s = torch.sigmoid(g)
+    t_u = torch.tanh(u / linear_beta)
+    f = beta * t_g * s
+    df = (1.0 - t_g.square()) * s + beta * t_g * s * (1.0 - s)
+    return linear_beta * t_u * df, f * (1.0 - t_u.square())
+
+
 @dataclass(frozen=True)
 class CoupledHadamardSpec:
     """Transform parameters of a coupled profile (reference :26-46)."""
@@ -377,4 +395,5 @@ __all__ = [
     "rotation_signs",
     "signed_block_hadamard",
     "situ",
+    "situ_derivatives",
 ]
