@@ -18,11 +18,14 @@ import torch
 import torch.nn.functional as F
 
 from . import gemm
+from .qsrt_coupled import situ
 
 # Phase-1 policy constants (reference qsrt/qsrt.py:228-233)
 PHASE1_H13_EXPERT_LOCAL_ALPHA = 0.0
 PHASE1_H2_EXPERT_LOCAL_ALPHA = 0.75
 PHASE1_H2_SHRINKAGE_POLICY = "weighted_oas_scaled_identity"
+# Candidate-encode Hessian policies (reference qsrt/pack/qsrt_candidates.py:67-68)
+HESSIAN_POLICIES = ("captured_blend", "identity")
 
 
 def partition_documents(documents: Sequence[str], *, modulus: int, confirmation_index: int):
@@ -267,3 +270,36 @@ def build_expert_hessians(inputs: torch.Tensor, gates: torch.Tensor, source_midd
         evidence = {"h2_shrinkage_policy": "fixed_alpha_scaled_identity", "h2_local_alpha": float(h2_alpha),
                     "h2_local_alpha_cap": float(h2_alpha), "h2_identity_scale": scale}
     return h13, h2, {"gate_square_sum": h13_weight, "h13_local_alpha": float(h13_alpha), **evidence}
+
+
+def _candidate_middle_by_r13(inputs: torch.Tensor, upstream, evaluated_modes) -> dict[int, torch.Tensor]:
+    """Post-SiTU rows of each upstream rate's decoded gate/up reconstruction
+    (``upstream["w1"][r13].reconstruction`` and ``["w3"]``, reference
+    qsrt/pack/qsrt_candidates.py:406-419)."""
+
+    return {int(r13): situ(F.linear(inputs, upstream["w1"][int(r13)].reconstruction),
+                           F.linear(inputs, upstream["w3"][int(r13)].reconstruction)) for r13 in evaluated_modes}
+
+
+def _conditional_h2_by_r13(inputs: torch.Tensor, gates: torch.Tensor, fit_mask_device: torch.Tensor,
+                           middle_by_r13: dict[int, torch.Tensor], *, global_h13: torch.Tensor,
+                           global_h2: torch.Tensor, device: torch.device, hessian_policy: str,
+                           have_local_support: bool):
+    """One down-projection H2 per upstream rate from that rate's decoded rows
+    over the fit rows, or the identity under the ``"identity"`` policy or
+    without local support (reference qsrt/pack/qsrt_candidates.py:422-461)."""
+
+    h2_by_r13: dict[int, torch.Tensor] = {}
+    evidence: dict[str, object] = {}
+    identity = torch.eye(global_h2.shape[0], dtype=torch.float32, device=device)
+    for r13, middle in middle_by_r13.items():
+        if hessian_policy == "identity" or not have_local_support:
+            h2_by_r13[r13] = identity
+            evidence[f"R{r13}"] = {"h2_shrinkage_policy": "identity_fallback", "h2_local_alpha": 0.0,
+                                   "h2_effective_sample_size": 0.0, "h2_identity_scale": 1.0}
+            continue
+        _, h2, ev = build_expert_hessians(inputs[fit_mask_device], gates[fit_mask_device], middle[fit_mask_device],
+                                          global_h13=global_h13, global_h2=global_h2, device=device)
+        h2_by_r13[r13] = h2
+        evidence[f"R{r13}"] = ev
+    return h2_by_r13, evidence

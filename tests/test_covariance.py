@@ -190,3 +190,39 @@ def test_build_expert_hessians_policies():
     assert ev["h2_shrinkage_policy"] == "fixed_alpha_scaled_identity"
     with pytest.raises(ValueError, match="dimension"):
         ch.build_expert_hessians(inputs, gates, middle, global_h13=global_h13, global_h2=torch.zeros(5, 5), device=CPU)
+
+
+def test_conditional_h2_per_upstream_rate():
+    from types import SimpleNamespace
+
+    from qsrt_amd.qsrt_coupled import situ
+
+    inputs = torch.tensor([[1.0, 0.0], [0.0, 1.0], [1.0, 1.0], [-1.0, 0.5]])
+    gates = torch.tensor([1.0, 0.75, 0.5, 0.25])
+    upstream = {"w1": {0: SimpleNamespace(reconstruction=torch.eye(2)),
+                       1: SimpleNamespace(reconstruction=2.0 * torch.eye(2))},
+                "w3": {0: SimpleNamespace(reconstruction=torch.eye(2)),
+                       1: SimpleNamespace(reconstruction=torch.tensor([[1.0, 1.0], [0.0, 1.0]]))}}
+    middle = ch._candidate_middle_by_r13(inputs, upstream, (0, 1))
+    torch.testing.assert_close(middle[0], situ(inputs, inputs))
+    torch.testing.assert_close(middle[1], situ(2.0 * inputs, inputs @ torch.tensor([[1.0, 1.0], [0.0, 1.0]]).T))
+    mask = torch.tensor([True, True, False, True])
+    h2, ev = ch._conditional_h2_by_r13(inputs, gates, mask, middle, global_h13=torch.eye(2), global_h2=torch.eye(2),
+                                       device=CPU, hessian_policy="captured_blend", have_local_support=True)
+    assert set(h2) == {0, 1} and not torch.allclose(h2[0], h2[1])
+    for r in (0, 1):
+        local, _ = ch.weighted_covariance(middle[r][mask], gates[mask].square(), device=CPU)
+        want, s = ch.adaptive_identity_shrinkage(local, gates[mask].square())
+        torch.testing.assert_close(h2[r], want)
+        assert ev[f"R{r}"]["h2_shrinkage_policy"] == "weighted_oas_scaled_identity"
+    assert ev["R1"]["h2_effective_sample_size"] == pytest.approx(ev["R0"]["h2_effective_sample_size"])
+    # pooled global H2 values never enter
+    other, _ = ch._conditional_h2_by_r13(inputs, gates, mask, middle, global_h13=torch.eye(2),
+                                         global_h2=5.0 * torch.ones(2, 2), device=CPU,
+                                         hessian_policy="captured_blend", have_local_support=True)
+    torch.testing.assert_close(other[0], h2[0])
+    for policy, support in (("identity", True), ("captured_blend", False)):
+        fallback, ev = ch._conditional_h2_by_r13(inputs, gates, mask, middle, global_h13=torch.eye(2),
+                                                 global_h2=torch.eye(2), device=CPU, hessian_policy=policy,
+                                                 have_local_support=support)
+        assert torch.equal(fallback[1], torch.eye(2)) and ev["R1"]["h2_shrinkage_policy"] == "identity_fallback"
