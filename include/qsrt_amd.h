@@ -40,7 +40,8 @@ size_t qsrt_viterbi_workspace_bytes(int K, int64_t n_tiles);
  *   tiles   f32 [n_tiles, 256]  targets in tensor-core order
  *   recon   f32 [n_tiles, 256]  out: E4M3 label of each emitted codeword
  *   states  u16 [n_tiles, 256]  out: 16-bit codewords (closed cyclic path)
- *   K       2, 3 or 4 branch bits per weight
+ *   K       1 .. 6 branch bits per weight (the reference's K1..K6 dispatch,
+ *           qsrt/csrc/sqg_quantize.cu:720-780)
  *   tailbite_context  1..128 primer half-width C
  *   lut_e4m3  u8 [65536] state(codeword)-indexed E4M3 labels
  *   boundary_lag  0: boundary = argmin of the primer's final costs

@@ -7,7 +7,8 @@
 //   * one 256-weight tile per workgroup of 1024 threads (16 wave64s), one
 //     workgroup per CU, persistent over a strided tile range;
 //   * FP32 path metrics ping-pong in LDS (2 * 2^(16-K) floats: 128 KiB at
-//     K2, 64 KiB at K3, 32 KiB at K4);
+//     K2, 64 KiB at K3, 32 KiB at K4, down to 8 KiB at K6); K1's 2^15
+//     states use one 128 KiB array updated in place;
 //   * each thread owns 64 trellis edges for the whole kernel: the 2^K
 //     predecessors of a few states, whose E4M3 labels are widened to FP32
 //     once and kept in VGPRs;
@@ -15,8 +16,10 @@
 //     every LDS cost read serves 2^K edges;
 //   * per state: d = label - x, c = fma(d, d, cost[pred]), value = min3
 //     chain, decision = lowest k with c == value (lowest-index ties);
-//   * decisions are packed (2 bits at K2, a nibble at K3/K4) into one
-//     coalesced store per thread per step, in a per-workgroup HBM buffer;
+//   * K5 / K6 (32 / 64 predecessors per state) stream the predecessors
+//     through a running minimum instead of holding them in registers;
+//   * decisions are packed (K bits per state, 1..32 bits per thread) into
+//     one coalesced store per thread per step, in a per-workgroup HBM buffer;
 //   * the boundary argmin is a wave64 shuffle reduction with lowest-index
 //     ties;
 //   * passes are pipelined over two tiles per workgroup (P0, P1, F0, P2,
@@ -37,6 +40,22 @@ constexpr int kWaves = kThreads / 64;
 
 template <int K>
 struct Geo;
+
+// K1: 32768 states, groups of 2 states with predecessors q + 16384 k.
+// Thread t owns groups q = t + 1024 j (j < 16); 32 one-bit decisions.  Two
+// FP32 cost arrays would need 256 KiB of LDS, so K1 updates one array in
+// place (every predecessor cost is read into registers before a barrier,
+// then the new costs are written).
+template <>
+struct Geo<1> {
+    static constexpr int S = 1 << 15, P = 2, NG = 16, NS = 2, kPredStride = 1 << 14;
+    static constexpr int kRowBytes = kThreads * 4;
+    __device__ static int group(int t, int j) { return t + kThreads * j; }
+    __device__ static int first_state(int t, int j) { return 2 * group(t, j); }
+    // field f = 2 j + e sits at bit 31 - f
+    __device__ static int word_index(int s) { return (s >> 1) & (kThreads - 1); }
+    __device__ static int extract(uint32_t w, int s) { return (w >> (31 - (2 * (s >> 11) + (s & 1)))) & 1; }
+};
 
 // K2: 16384 states, groups of 4 states with predecessors q + 4096 k.
 // Thread t owns groups q = t + 1024 j (j < 4).
@@ -78,6 +97,36 @@ struct Geo<4> {
     __device__ static int extract(uint32_t w, int s) { return (w >> (16 * ((s >> 2) & 1) + 4 * (3 - (s & 3)))) & 15; }
 };
 
+// K5: 2048 states, groups of 32 states with predecessors q + 64 k.
+// Thread t owns states 2t, 2t+1 (group q = t >> 4); 10 decision bits in a
+// 16-bit field, state 2 t + e at bits [5 (1 - e), +5).
+template <>
+struct Geo<5> {
+    static constexpr int S = 1 << 11, P = 32, NG = 1, NS = 2, kPredStride = 1 << 6;
+    static constexpr int kRowBytes = kThreads * 2;
+    __device__ static int group(int t, int) { return t >> 4; }
+    __device__ static int first_state(int t, int) { return 2 * t; }
+    __device__ static int word_index(int s) { return s >> 2; }
+    __device__ static int extract(uint32_t w, int s) { return (w >> (16 * ((s >> 1) & 1) + 5 * (1 - (s & 1)))) & 31; }
+};
+
+// K6: 1024 states, groups of 64 states with predecessors q + 16 k.
+// Thread t owns state t (group q = t >> 6, uniform over a wave); one byte
+// per thread holds its 6-bit decision.
+template <>
+struct Geo<6> {
+    static constexpr int S = 1 << 10, P = 64, NG = 1, NS = 1, kPredStride = 1 << 4;
+    static constexpr int kRowBytes = kThreads;
+    __device__ static int group(int t, int) { return t >> 6; }
+    __device__ static int first_state(int t, int) { return t; }
+    __device__ static int word_index(int s) { return s >> 2; }
+    __device__ static int extract(uint32_t w, int s) { return (w >> (8 * (s & 3))) & 63; }
+};
+
+// Cost arrays in LDS: ping-pong pairs, except K1 (in place).
+template <int K>
+constexpr int kCostArrays = K == 1 ? 1 : 2;
+
 // Decision word holding state s at tile position `pos` (workgroup-scope:
 // the writers are this workgroup's other waves, fenced before a barrier).
 template <int K>
@@ -89,6 +138,14 @@ __device__ __forceinline__ uint32_t load_decisions(const uint8_t* dec, int pos, 
 template <int K>
 struct Labels {
     float v[Geo<K>::NG][Geo<K>::NS][Geo<K>::P];
+};
+
+// K1 keeps its labels as fp16 pairs (E4M3 values are exact in fp16): its 32
+// predecessor costs must sit in registers across the in-place barrier too.
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+template <>
+struct Labels<1> {
+    f16x2 v[Geo<1>::NG][Geo<1>::NS];
 };
 
 __device__ __forceinline__ float fmin2(float a, float b) { return __builtin_fminf(a, b); }
@@ -134,16 +191,111 @@ __device__ __forceinline__ uint32_t push_argmin(uint32_t word, const float (&c)[
     return word;
 }
 
-// One trellis step over all states.  On the first step of a pass (FIRST)
-// there are no predecessor costs: every predecessor starts at 0, or, in the
-// constrained pass, only `pre_state` starts at 0 and the others at +inf
+// Predecessor cost of the first step of a pass: 0 for every predecessor, or,
+// in the constrained pass, 0 for `pre_state` and +inf for the others
 // (fma(d, d, 0) == d * d and fma(d, d, inf) == inf, so this is exactly the
-// reference's step-0 rule).  RECORD: pack and store this row's decisions.
+// reference's step-0 rule).
+__device__ __forceinline__ float first_cost(int pred, int pre_state) {
+    return (pre_state < 0 || pred == pre_state) ? 0.0f : __builtin_inff();
+}
+
+// K1 step on the single in-place cost array: the thread's 32 predecessor
+// costs are read into registers, a barrier orders every read before any
+// write, then the 32 new costs are written over them.
+template <bool RECORD, bool FIRST>
+__device__ __forceinline__ void trellis_step_k1(const Labels<1>& lab, float* cost, float x, int pre_state,
+                                                uint8_t* __restrict__ dec_row, int t) {
+    using G = Geo<1>;
+    float p[G::NG][G::P];
+#pragma unroll
+    for (int j = 0; j < G::NG; ++j)
+#pragma unroll
+        for (int k = 0; k < G::P; ++k) {
+            const int pred = G::group(t, j) + k * G::kPredStride;
+            p[j][k] = FIRST ? first_cost(pred, pre_state) : cost[pred];
+        }
+    if constexpr (!FIRST) __syncthreads();
+    // Widen the fp16 labels here, per step: hoisted out of the pass loop,
+    // 64 FP32 copies would not fit beside the predecessor costs.
+    f16x2 h[G::NG][G::NS];
+#pragma unroll
+    for (int j = 0; j < G::NG; ++j)
+#pragma unroll
+        for (int e = 0; e < G::NS; ++e) {
+            h[j][e] = lab.v[j][e];
+            asm volatile("" : "+v"(h[j][e]));
+        }
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < G::NG; ++j) {
+        float best[G::NS];
+#pragma unroll
+        for (int e = 0; e < G::NS; ++e) {
+            float c[G::P];
+#pragma unroll
+            for (int k = 0; k < G::P; ++k) {
+                const float d = static_cast<float>(h[j][e][k]) - x;
+                c[k] = __builtin_fmaf(d, d, p[j][k]);
+            }
+            best[e] = fmin2(c[0], c[1]);
+            if constexpr (RECORD) word = push_argmin<1>(word, c, best[e]);
+        }
+        *reinterpret_cast<float2*>(cost + G::first_state(t, j)) = make_float2(best[0], best[1]);
+    }
+    if constexpr (RECORD) reinterpret_cast<uint32_t*>(dec_row)[t] = word;
+}
+
+// K5 / K6 step: 32 or 64 predecessors per state, streamed one at a time
+// with a running minimum and its lowest index (strict less-than while k
+// increases), so neither the predecessor costs nor the candidate costs have
+// to sit in registers together with the thread's 64 labels.
+template <int K, bool RECORD, bool FIRST>
+__device__ __forceinline__ void trellis_step_wide(const Labels<K>& lab, const float* __restrict__ prev,
+                                                  float* __restrict__ next, float x, int pre_state,
+                                                  uint8_t* __restrict__ dec_row, int t) {
+    using G = Geo<K>;
+    const int q = G::group(t, 0);
+    float m[G::NS];
+    int arg[G::NS];
+#pragma unroll
+    for (int k = 0; k < G::P; ++k) {
+        const int pred = q + k * G::kPredStride;
+        const float p = FIRST ? first_cost(pred, pre_state) : prev[pred];
+#pragma unroll
+        for (int e = 0; e < G::NS; ++e) {
+            const float d = lab.v[0][e][k] - x;
+            const float c = __builtin_fmaf(d, d, p);
+            if (k == 0) {
+                m[e] = c;
+                arg[e] = 0;
+            } else {
+                const bool lt = c < m[e];
+                m[e] = lt ? c : m[e];
+                arg[e] = lt ? k : arg[e];
+            }
+        }
+    }
+    if constexpr (G::NS == 2) {
+        *reinterpret_cast<float2*>(next + G::first_state(t, 0)) = make_float2(m[0], m[1]);
+        if constexpr (RECORD) reinterpret_cast<uint16_t*>(dec_row)[t] = static_cast<uint16_t>((arg[0] << K) | arg[1]);
+    } else {
+        next[G::first_state(t, 0)] = m[0];
+        if constexpr (RECORD) dec_row[t] = static_cast<uint8_t>(arg[0]);
+    }
+}
+
+// One trellis step over all states.  FIRST: the pass's first step (see
+// first_cost).  RECORD: pack and store this row's decisions.
 template <int K, bool RECORD, bool FIRST>
 __device__ __forceinline__ void trellis_step(const Labels<K>& lab, const float* __restrict__ prev,
                                              float* __restrict__ next, float x, int pre_state,
                                              uint8_t* __restrict__ dec_row, int t) {
     using G = Geo<K>;
+    if constexpr (K == 1) {
+        trellis_step_k1<RECORD, FIRST>(lab, next, x, pre_state, dec_row, t);  // prev == next
+    } else if constexpr (K >= 5) {
+        trellis_step_wide<K, RECORD, FIRST>(lab, prev, next, x, pre_state, dec_row, t);
+    } else {
     uint32_t word = 0;
 #pragma unroll
     for (int j = 0; j < G::NG; ++j) {
@@ -151,8 +303,7 @@ __device__ __forceinline__ void trellis_step(const Labels<K>& lab, const float* 
         float p[G::P];
         if constexpr (FIRST) {
 #pragma unroll
-            for (int k = 0; k < G::P; ++k)
-                p[k] = (pre_state < 0 || q + k * G::kPredStride == pre_state) ? 0.0f : __builtin_inff();
+            for (int k = 0; k < G::P; ++k) p[k] = first_cost(q + k * G::kPredStride, pre_state);
         } else {
 #pragma unroll
             for (int k = 0; k < G::P; ++k) p[k] = prev[q + k * G::kPredStride];
@@ -197,6 +348,7 @@ __device__ __forceinline__ void trellis_step(const Labels<K>& lab, const float* 
         else
             reinterpret_cast<uint32_t*>(dec_row)[t] = word;
     }
+    }  // K2..K4
 }
 
 // Lowest-index argmin of `cost` over all states; result valid in thread 0.
@@ -301,12 +453,15 @@ struct TraceJob {
 
 // One forward pass of `steps` steps over positions roll, roll+1, ... (mod
 // 256), recording decisions from step `trace_start` on, with the pending
-// traceback `job` advanced one position per step by lane 0.
+// traceback `job` advanced one position per step by lane 0.  `fresh`: the
+// first step starts the pass (first_cost); otherwise the pass continues
+// from the costs already in LDS.
 template <int K>
 __device__ __forceinline__ void forward_pass(const Labels<K>& lab, const float* sx, float*& prev, float*& next, int roll,
                                              int steps, int pre_state, int trace_start, uint8_t* dec, int t,
-                                             TraceJob& job) {
-    {
+                                             TraceJob& job, bool fresh = true) {
+    int i = 0;
+    if (fresh) {
         const int pos = roll & (kTile - 1);
         uint8_t* row = dec + static_cast<size_t>(pos) * Geo<K>::kRowBytes;
         if (trace_start == 0)
@@ -316,8 +471,9 @@ __device__ __forceinline__ void forward_pass(const Labels<K>& lab, const float* 
         if (job.kind && t == 0 && job.pos >= 0) trace_advance<K>(job.dec, job.words, job.pos, job.edge, job.pending);
         __syncthreads();
         float* tmp = prev; prev = next; next = tmp;
+        i = 1;
     }
-    for (int i = 1; i < steps; ++i) {
+    for (; i < steps; ++i) {
         const int pos = (i + roll) & (kTile - 1);
         uint8_t* row = dec + static_cast<size_t>(pos) * Geo<K>::kRowBytes;
         if (i >= trace_start)
@@ -366,8 +522,7 @@ __global__ __launch_bounds__(kThreads, 1) void viterbi_tiles_kernel(
     int64_t n_tiles, int context, const uint8_t* __restrict__ lut, int boundary_lag,
     uint8_t* __restrict__ dec_ws) {
     using G = Geo<K>;
-    __shared__ __align__(16) float cost_a[G::S];
-    __shared__ __align__(16) float cost_b[G::S];
+    __shared__ __align__(16) float costs[kCostArrays<K> * G::S];
     __shared__ float sx[2][kTile];
     __shared__ uint16_t words[2][kTile];
     __shared__ int end_state[2];
@@ -386,7 +541,8 @@ __global__ __launch_bounds__(kThreads, 1) void viterbi_tiles_kernel(
         for (int e = 0; e < G::NS; ++e)
 #pragma unroll
             for (int k = 0; k < G::P; ++k)
-                lab.v[j][e][k] = qsrt::e4m3_to_float(lut[(k << (16 - K)) | (G::first_state(t, j) + e)]);
+                lab.v[j][e][k] = static_cast<decltype(+lab.v[j][e][k])>(
+                    qsrt::e4m3_to_float(lut[(k << (16 - K)) | (G::first_state(t, j) + e)]));
 
     // This workgroup's tiles are first + i * stride, i < m.  Passes run in
     // the order P0, P1, F0, P2, F1, ..., F(m-1) (primer of tile i+1 before
@@ -424,10 +580,19 @@ __global__ __launch_bounds__(kThreads, 1) void viterbi_tiles_kernel(
 
         // Primer: positions 256-C .. 255, 0 .. C-1, decisions kept for 0 .. C-1.
         // Constrained pass: positions 0 .. 255 from the boundary state.
-        float* prev = cost_a;
-        float* next = cost_b;
-        forward_pass<K>(lab, sx[slot], prev, next, primer ? kTile - context : 0, primer ? 2 * context : kTile,
-                        primer ? -1 : end_state[slot], primer ? context : 0, dec, t, job);
+        float* prev = costs;
+        float* next = costs + (kCostArrays<K> - 1) * G::S;
+        int start_in_place = 0;  // K1, boundary lag 1: argmin of the penultimate primer costs (thread 0)
+        if (kCostArrays<K> == 1 && primer && boundary_lag) {
+            // The single array still holds the penultimate costs after 2C - 1
+            // steps: take their argmin there, then run the last, recorded step.
+            forward_pass<K>(lab, sx[slot], prev, next, kTile - context, 2 * context - 1, -1, context, dec, t, job);
+            start_in_place = boundary_argmin<K>(prev, red_v, red_i, t);  // has a barrier
+            forward_pass<K>(lab, sx[slot], prev, next, kTile + context - 1, 1, -1, 0, dec, t, job, false);
+        } else {
+            forward_pass<K>(lab, sx[slot], prev, next, primer ? kTile - context : 0, primer ? 2 * context : kTile,
+                            primer ? -1 : end_state[slot], primer ? context : 0, dec, t, job);
+        }
 
         // Close the traceback that ran alongside this pass.
         if (job.kind) {
@@ -441,7 +606,9 @@ __global__ __launch_bounds__(kThreads, 1) void viterbi_tiles_kernel(
         // writer and readers share one CU, so workgroup scope suffices.
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         if (primer) {
-            const int start = boundary_argmin<K>(boundary_lag ? next : prev, red_v, red_i, t);  // has a barrier
+            const int start = (kCostArrays<K> == 1 && boundary_lag)
+                                  ? start_in_place
+                                  : boundary_argmin<K>(boundary_lag ? next : prev, red_v, red_i, t);  // has a barrier
             if (t == 0) bcast = start;
             __syncthreads();
             start_job<K>(job, 1, i, dec, nullptr, context - 1, bcast, t);
@@ -464,9 +631,12 @@ size_t row_bytes() { return static_cast<size_t>(Geo<K>::kRowBytes); }
 
 size_t workgroup_dec_bytes(int K) {
     switch (K) {
+        case 1: return 2 * kTile * row_bytes<1>();
         case 2: return 2 * kTile * row_bytes<2>();
         case 3: return 2 * kTile * row_bytes<3>();
         case 4: return 2 * kTile * row_bytes<4>();
+        case 5: return 2 * kTile * row_bytes<5>();
+        case 6: return 2 * kTile * row_bytes<6>();
         default: return 0;
     }
 }
@@ -490,8 +660,8 @@ int qsrt_viterbi_tiles(const float* tiles, float* recon, uint16_t* states, int64
                        int tailbite_context, const uint8_t* lut_e4m3, int boundary_lag, void* workspace,
                        size_t workspace_bytes, void* stream_handle) {
     hipStream_t stream = static_cast<hipStream_t>(stream_handle);
-    if (K < 2 || K > 4)
-        return qsrt::fail(qsrt::kBadArgument, "K%d is not supported by the MI355X tile kernel (K2..K4)", K);
+    if (K < 1 || K > 6)
+        return qsrt::fail(qsrt::kBadArgument, "K%d is not supported by the MI355X tile kernel (K1..K6)", K);
     if (tailbite_context < 1 || tailbite_context > 128)
         return qsrt::fail(qsrt::kBadArgument, "tailbite_context must be in 1..128");
     if (boundary_lag != 0 && boundary_lag != 1)
@@ -507,20 +677,20 @@ int qsrt_viterbi_tiles(const float* tiles, float* recon, uint16_t* states, int64
     if (workspace_bytes < need)
         return qsrt::fail(qsrt::kWorkspaceTooSmall, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
     auto* ws = static_cast<uint8_t*>(workspace);
+#define QSRT_LAUNCH_VITERBI(KK)                                                                                  \
+    case KK:                                                                                                     \
+        hipLaunchKernelGGL(viterbi_tiles_kernel<KK>, dim3(grid), dim3(kThreads), 0, stream, tiles, recon, states, \
+                           n_tiles, tailbite_context, lut_e4m3, boundary_lag, ws);                             \
+        break;
     switch (K) {
-        case 2:
-            hipLaunchKernelGGL(viterbi_tiles_kernel<2>, dim3(grid), dim3(kThreads), 0, stream, tiles, recon, states,
-                               n_tiles, tailbite_context, lut_e4m3, boundary_lag, ws);
-            break;
-        case 3:
-            hipLaunchKernelGGL(viterbi_tiles_kernel<3>, dim3(grid), dim3(kThreads), 0, stream, tiles, recon, states,
-                               n_tiles, tailbite_context, lut_e4m3, boundary_lag, ws);
-            break;
-        default:
-            hipLaunchKernelGGL(viterbi_tiles_kernel<4>, dim3(grid), dim3(kThreads), 0, stream, tiles, recon, states,
-                               n_tiles, tailbite_context, lut_e4m3, boundary_lag, ws);
-            break;
+        QSRT_LAUNCH_VITERBI(1)
+        QSRT_LAUNCH_VITERBI(2)
+        QSRT_LAUNCH_VITERBI(3)
+        QSRT_LAUNCH_VITERBI(4)
+        QSRT_LAUNCH_VITERBI(5)
+        QSRT_LAUNCH_VITERBI(6)
     }
+#undef QSRT_LAUNCH_VITERBI
     QSRT_HIP_TRY(hipGetLastError());
     return qsrt::kOk;
 }

@@ -113,8 +113,8 @@ def viterbi_tiles(
 
     if not tiles.is_cuda:
         raise ValueError("the MI355X tile quantizer requires a GPU tensor")
-    if bits not in (2, 3, 4):
-        raise ValueError(f"K{bits} is not supported by the MI355X tile kernel (K2..K4)")
+    if bits not in (1, 2, 3, 4, 5, 6):
+        raise ValueError(f"K{bits} is not supported by the MI355X tile kernel (K1..K6)")
     tiles = tiles.contiguous()
     if tiles.dtype != torch.float32 or tiles.ndim != 2 or tiles.shape[1] != 256:
         raise ValueError("SQG tiles must be contiguous FP32 [N, 256]")
@@ -211,8 +211,8 @@ def quantize_tiles_sqg(tiles: torch.Tensor, quant_args: dict) -> tuple[torch.Ten
     if quant_args.get("return_trellis_diagnostics"):
         raise NotImplementedError("on-GPU trellis diagnostics are a research feature outside the MI355X hot path")
     bits = int(quant_args["K"])
-    if bits not in (2, 3, 4):
-        raise NotImplementedError(f"K{bits} is not supported by the MI355X tile kernel (K2..K4)")
+    if bits not in (1, 2, 3, 4, 5, 6):
+        raise ValueError(f"SQG tile quantization supports K1 through K6, not K{bits}")
     lut = _resolve_codebook(quant_args, bits, tiles.device)
     lag = boundary_lag(bits, _lut_abs_max(lut), quant_args.get("tailbite_boundary", "reference"))
     context = int(quant_args.get("tailbite_context", 128))

@@ -25,6 +25,8 @@ import torch
 SMALL = [
     (6, 2, 8, 1), (6, 2, 8, 2), (6, 2, 8, 4), (6, 3, 6, 2), (6, 3, 6, 3),
     (4, 1, 8, 2), (4, 1, 8, 4), (8, 2, 6, 3), (8, 4, 4, 2), (8, 3, 4, 2),
+    # 32 and 64 predecessors per state (the K5 / K6 trellis shape)
+    (10, 5, 2, 1), (10, 5, 3, 1), (12, 6, 2, 1), (12, 6, 3, 1),
 ]
 
 
@@ -59,7 +61,7 @@ def test_planted_tie_rule_mistake_is_detected():
     assert disagreements > 0
 
 
-@pytest.mark.parametrize("bits", (2, 3, 4))
+@pytest.mark.parametrize("bits", (1, 2, 3, 4, 5, 6))
 @pytest.mark.parametrize("context", (1, 32, 128))
 def test_oracle_production_size_closure(bits, context):
     rng = np.random.default_rng(bits * 10 + context)

@@ -1,7 +1,7 @@
 """GPU parity of the HIP tile Viterbi against the CPU oracle.
 
 Bar: states (codewords) and reconstructions bit-exact with
-oracle/viterbi_ref.c on the same seeded inputs, for K2/K3/K4, tail-bite
+oracle/viterbi_ref.c on the same seeded inputs, for K1..K6, tail-bite
 contexts 1/32/128 and both boundary rules, plus the reference's own GPU
 checks (closure, decode, saturated inputs; reference
 tests/test_sqg_quantizer.py:178-231).
@@ -37,7 +37,7 @@ def _gpu(tiles: np.ndarray, bits: int, context: int, lag: int):
 
 @pytest.mark.parametrize("lag", (0, 1))
 @pytest.mark.parametrize("context", (1, 32, 128))
-@pytest.mark.parametrize("bits", (2, 3, 4))
+@pytest.mark.parametrize("bits", (1, 2, 3, 4, 5, 6))
 def test_gpu_matches_oracle_bit_exact(bits, context, lag):
     _say(f"[viterbi] K{bits} C{context} lag{lag}: 24 tiles")
     rng = np.random.default_rng(100 * bits + context + lag)
@@ -52,7 +52,7 @@ def test_gpu_matches_oracle_bit_exact(bits, context, lag):
     assert np.array_equal(recon, o_recon)
 
 
-@pytest.mark.parametrize("bits", (2, 3, 4))
+@pytest.mark.parametrize("bits", (1, 2, 3, 4, 5, 6))
 def test_gpu_many_tiles_persistent_loop(bits):
     """More tiles than workgroups: every workgroup walks several tiles."""
 
@@ -119,7 +119,8 @@ def test_bad_arguments_raise():
     lut = sqg_xor_cheb_t12_bytes(2).cuda()
     with pytest.raises(ValueError):
         viterbi_tiles(torch.zeros((1, 128), device="cuda"), lut, 2)
-    with pytest.raises(ValueError):
-        viterbi_tiles(torch.zeros((1, 256), device="cuda"), lut, 5)
+    for bits in (0, 7):
+        with pytest.raises(ValueError):
+            viterbi_tiles(torch.zeros((1, 256), device="cuda"), lut, bits)
     with pytest.raises(ValueError):
         viterbi_tiles(torch.zeros((1, 256), device="cuda"), lut, 2, tailbite_context=129)
