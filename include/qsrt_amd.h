@@ -58,7 +58,8 @@ int qsrt_viterbi_tiles(const float *tiles, float *recon, uint16_t *states, int64
                        size_t workspace_bytes, void *stream);
 
 /*
- * EXL word packing of n_tiles tiles at rate K (2..4):
+ * EXL word packing of n_tiles tiles at rate K (1..6; the QSRT container uses
+ * 2..4, the uniform codec paths of qsrt/qsrt_codec_pilot.py:220-281 up to 6):
  *   states u16 [n_tiles, 256] (only the low K bits are stored; 16-byte
  *   aligned), words i16 [n_tiles, 16 K] out.
  * Replaces the un-vendored ext.pack_trellis called from
@@ -69,7 +70,7 @@ int qsrt_pack_edges(const uint16_t *states, int64_t n_tiles, int K, int16_t *wor
 
 /*
  * Inverse of qsrt_pack_edges followed by the cyclic state closed form:
- *   words i16 [n_tiles, 16 K] -> states u16 [n_tiles, 256].
+ *   words i16 [n_tiles, 16 K] -> states u16 [n_tiles, 256], K 1..6.
  * Replaces unpack_trellis_states (qsrt/qsrt.py:910-913) =
  * unpack_trellis_edges (:886-907) + reconstruct_trellis_states
  * (qsrt/exl3_reference.py:34-58).

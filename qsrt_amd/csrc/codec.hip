@@ -14,7 +14,8 @@ namespace {
 
 constexpr int kTile = 256;
 
-// One thread per 16-symbol span: 16 K bits -> K words.
+// One thread per 16-symbol span: 16 K bits -> K words, emitted as soon as
+// 16 bits have accumulated (the accumulator never holds more than 15 + K).
 template <int K>
 __global__ __launch_bounds__(256) void pack_edges_kernel(const uint16_t* __restrict__ states, int64_t n_spans,
                                                         uint16_t* __restrict__ words) {
@@ -23,19 +24,22 @@ __global__ __launch_bounds__(256) void pack_edges_kernel(const uint16_t* __restr
     const uint4* src = reinterpret_cast<const uint4*>(states + g * 16);
     const uint4 a = src[0], b = src[1];
     const uint32_t halves[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    uint64_t acc = 0;
+    const int64_t tile = g >> 4;
+    const int span = static_cast<int>(g & 15);
+    uint16_t* out = words + tile * (16 * K);
+    uint32_t acc = 0;
+    int held = 0, w = 0;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const uint32_t sym = (halves[i >> 1] >> (16 * (i & 1))) & ((1u << K) - 1);
         acc = (acc << K) | sym;
-    }
-    const int64_t tile = g >> 4;
-    const int span = static_cast<int>(g & 15);
-    uint16_t* out = words + tile * (16 * K);
-#pragma unroll
-    for (int w = 0; w < K; ++w) {
-        const int idx = span * K + w;
-        out[idx ^ 1] = static_cast<uint16_t>(acc >> (16 * (K - 1 - w)));
+        held += K;
+        if (held >= 16) {
+            held -= 16;
+            out[(span * K + w) ^ 1] = static_cast<uint16_t>(acc >> held);
+            acc &= (1u << held) - 1;
+            ++w;
+        }
     }
 }
 
@@ -67,7 +71,7 @@ extern "C" {
 
 int qsrt_pack_edges(const uint16_t* states, int64_t n_tiles, int K, int16_t* words, void* stream_handle) {
     hipStream_t stream = static_cast<hipStream_t>(stream_handle);
-    if (K < 2 || K > 4) return qsrt::fail(qsrt::kBadArgument, "K%d packing is not supported (K2..K4)", K);
+    if (K < 1 || K > 6) return qsrt::fail(qsrt::kBadArgument, "K%d packing is not supported (K1..K6)", K);
     if (n_tiles < 0) return qsrt::fail(qsrt::kBadArgument, "n_tiles must be non-negative");
     if (n_tiles == 0) return qsrt::kOk;
     if (!states || !words) return qsrt::fail(qsrt::kBadArgument, "null pointer argument");
@@ -76,29 +80,27 @@ int qsrt_pack_edges(const uint16_t* states, int64_t n_tiles, int K, int16_t* wor
     const int64_t spans = n_tiles * 16;
     const dim3 grid(static_cast<unsigned>((spans + 255) / 256));
     auto* out = reinterpret_cast<uint16_t*>(words);
-    switch (K) {
-        case 2: hipLaunchKernelGGL(pack_edges_kernel<2>, grid, dim3(256), 0, stream, states, spans, out); break;
-        case 3: hipLaunchKernelGGL(pack_edges_kernel<3>, grid, dim3(256), 0, stream, states, spans, out); break;
-        default: hipLaunchKernelGGL(pack_edges_kernel<4>, grid, dim3(256), 0, stream, states, spans, out); break;
-    }
+#define QSRT_PACK(KK) \
+    case KK: hipLaunchKernelGGL(pack_edges_kernel<KK>, grid, dim3(256), 0, stream, states, spans, out); break;
+    switch (K) { QSRT_PACK(1) QSRT_PACK(2) QSRT_PACK(3) QSRT_PACK(4) QSRT_PACK(5) QSRT_PACK(6) }
+#undef QSRT_PACK
     QSRT_HIP_TRY(hipGetLastError());
     return qsrt::kOk;
 }
 
 int qsrt_unpack_states(const int16_t* words, int64_t n_tiles, int K, uint16_t* states, void* stream_handle) {
     hipStream_t stream = static_cast<hipStream_t>(stream_handle);
-    if (K < 2 || K > 4) return qsrt::fail(qsrt::kBadArgument, "K%d unpacking is not supported (K2..K4)", K);
+    if (K < 1 || K > 6) return qsrt::fail(qsrt::kBadArgument, "K%d unpacking is not supported (K1..K6)", K);
     if (n_tiles < 0) return qsrt::fail(qsrt::kBadArgument, "n_tiles must be non-negative");
     if (n_tiles == 0) return qsrt::kOk;
     if (!states || !words) return qsrt::fail(qsrt::kBadArgument, "null pointer argument");
     if (n_tiles > 0x7fffffff) return qsrt::fail(qsrt::kBadArgument, "too many tiles for one launch");
     const auto* in = reinterpret_cast<const uint16_t*>(words);
     const dim3 grid(static_cast<unsigned>(n_tiles));
-    switch (K) {
-        case 2: hipLaunchKernelGGL(unpack_states_kernel<2>, grid, dim3(kTile), 0, stream, in, n_tiles, states); break;
-        case 3: hipLaunchKernelGGL(unpack_states_kernel<3>, grid, dim3(kTile), 0, stream, in, n_tiles, states); break;
-        default: hipLaunchKernelGGL(unpack_states_kernel<4>, grid, dim3(kTile), 0, stream, in, n_tiles, states); break;
-    }
+#define QSRT_UNPACK(KK) \
+    case KK: hipLaunchKernelGGL(unpack_states_kernel<KK>, grid, dim3(kTile), 0, stream, in, n_tiles, states); break;
+    switch (K) { QSRT_UNPACK(1) QSRT_UNPACK(2) QSRT_UNPACK(3) QSRT_UNPACK(4) QSRT_UNPACK(5) QSRT_UNPACK(6) }
+#undef QSRT_UNPACK
     QSRT_HIP_TRY(hipGetLastError());
     return qsrt::kOk;
 }
