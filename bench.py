@@ -417,19 +417,26 @@ def expert_bench(bits: int = 3, cpu_seconds: float = 4.0):
 MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "f32": 157.3}
 
 
-def _time_ms(fn, steps: int) -> float:
-    """Mean duration of ``fn`` over ``steps`` launches, HIP events on the
-    current stream (the stream the kernels are launched on)."""
+def _time_ms(fn, steps: int, min_ms: float = 2.0) -> float:
+    """Mean duration of ``fn`` over at least ``steps`` launches, HIP events on
+    the current stream (the stream the kernels are launched on).  Short
+    kernels get enough launches to fill ``min_ms`` of GPU time, so the mean
+    is the kernel's own duration rather than launch latency."""
 
     fn()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(steps):
+    fn()
+    e1.record()
+    torch.cuda.synchronize()
+    reps = max(steps, min(2000, math.ceil(min_ms / max(e0.elapsed_time(e1), 1e-3))))
+    e0.record()
+    for _ in range(reps):
         fn()
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
+    return e0.elapsed_time(e1) / reps
 
 
 def gemm_bench(steps: int = 5):

@@ -81,6 +81,23 @@ __global__ __launch_bounds__(kThreads) void hadamard_kernel(float* __restrict__ 
     const int64_t b0 = (tile % tiles_b) * O;
     const int64_t ext_b = LEFT ? cols : rows;
 
+    // Column rotations: a thread's four transformed indices a0 + 4 aq + i are
+    // the same in every load and store iteration (kThreads is a multiple of
+    // B / 4), so its multipliers are read once.
+    constexpr int AQ = B / 4;
+    static_assert(kThreads % AQ == 0, "column tiles need fixed transformed indices per thread");
+    float col_pre[4] = {1.f, 1.f, 1.f, 1.f}, col_div[4] = {1.f, 1.f, 1.f, 1.f};
+    float col_post[4] = {norm, norm, norm, norm};
+    if constexpr (!LEFT) {
+        const int64_t a = a0 + 4 * (t % AQ);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (pre_mul) col_pre[i] = pre_mul[a + i];
+            if (pre_div) col_div[i] = pre_div[a + i];
+            if (post_mul) col_post[i] = norm * post_mul[a + i];
+        }
+    }
+
     // ---- load (float4 along the contiguous axis), pre-scale, into LDS[a][b]
 #pragma unroll
     for (int k = 0; k < kTileElems / 4 / kThreads; ++k) {
@@ -90,25 +107,26 @@ __global__ __launch_bounds__(kThreads) void hadamard_kernel(float* __restrict__ 
             const int64_t col = b0 + 4 * bq;
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
             if (col < ext_b) v = *reinterpret_cast<const float4*>(x + (a0 + a) * ld + col);
-            float s = 1.0f;
-            if (pre_mul) s = pre_mul[a0 + a];
-            if (pre_div) {
-                v.x /= pre_div[a0 + a]; v.y /= pre_div[a0 + a];
-                v.z /= pre_div[a0 + a]; v.w /= pre_div[a0 + a];
-            }
+            float e[4] = {v.x, v.y, v.z, v.w};
+            const float m = pre_mul ? pre_mul[a0 + a] : 1.f;
+            const float dv = pre_div ? pre_div[a0 + a] : 1.f;
             float* d = lds + a * S + 4 * bq;
-            d[0] = v.x * s; d[1] = v.y * s; d[2] = v.z * s; d[3] = v.w * s;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (pre_mul) e[i] *= m;
+                if (pre_div) e[i] /= dv;
+                d[i] = e[i];
+            }
         } else {
-            const int b = f / (B / 4), aq = f % (B / 4);
+            const int b = f / AQ, aq = f % AQ;
             const int64_t row = b0 + b;
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
             if (row < ext_b) v = *reinterpret_cast<const float4*>(x + row * ld + a0 + 4 * aq);
             float e[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int64_t a = a0 + 4 * aq + i;
-                if (pre_mul) e[i] *= pre_mul[a];
-                if (pre_div) e[i] /= pre_div[a];
+                if (pre_mul) e[i] *= col_pre[i];
+                if (pre_div) e[i] /= col_div[i];
                 lds[(4 * aq + i) * S + b] = e[i];
             }
         }
@@ -132,16 +150,12 @@ __global__ __launch_bounds__(kThreads) void hadamard_kernel(float* __restrict__ 
             const float* d = lds + a * S + 4 * bq;
             *reinterpret_cast<float4*>(x + (a0 + a) * ld + col) = make_float4(d[0] * s, d[1] * s, d[2] * s, d[3] * s);
         } else {
-            const int b = f / (B / 4), aq = f % (B / 4);
+            const int b = f / AQ, aq = f % AQ;
             const int64_t row = b0 + b;
             if (row >= ext_b) continue;
             float e[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float s = norm;
-                if (post_mul) s *= post_mul[a0 + 4 * aq + i];
-                e[i] = lds[(4 * aq + i) * S + b] * s;
-            }
+            for (int i = 0; i < 4; ++i) e[i] = lds[(4 * aq + i) * S + b] * col_post[i];
             *reinterpret_cast<float4*>(x + row * ld + a0 + 4 * aq) = make_float4(e[0], e[1], e[2], e[3]);
         }
     }
