@@ -29,10 +29,11 @@
 //     of at most 128 x 6 on multiples of 2^-9).  The eight results of the
 //     tile-row stay in registers; the right H8 across tile-columns runs on
 //     VALU (exact: < 2^22 units of 2^-9).  Each value is split into fp16
-//     hi + lo (exact, 11 + 11 bits), and the right H16 is one f16 MFMA
-//     (16x16x32) per tile with k = [hi ; lo] and A = [H16 ; H16] with row i
-//     scaled by the fp16 sv of output column i.  Finally times su/128,
-//     conversion, four consecutive outputs per lane per tile.
+//     hi + lo (exact, 11 + 11 bits: hi by rounding, lo by a mixed-precision
+//     fma), and the right H16 is two accumulating f16 MFMAs (16x16x16) per
+//     tile, on hi then lo, sharing A = H16 with row i scaled by the fp16 sv
+//     of output column i.  Finally times su/128, conversion, four
+//     consecutive outputs per lane per tile.
 //  Memory traffic is shaped for the vector-memory pipe: a wave's 8 tiles of
 //  packed words arrive with one 16-byte load per lane and are staged through
 //  the wave's own slice of the LDS label area; outputs are staged through the
@@ -134,8 +135,22 @@ __device__ __forceinline__ u32x4 fetch_words(const BlockCtx& x, int w, int lane)
 }
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// fp16 pair {e0 - hi.x, e1 - hi.y} with hi a packed fp16 pair: each value is
+// one mixed-precision fma (fp16 source, fp32 addend, result rounded once to
+// fp16, v_fma_mixlo/mixhi_f16) written straight into its half of the result.
+// `neg_one` lives in a register so the fma is not rewritten as a subtraction,
+// which has no mixed-precision form; callers pass `hi` through an opaque copy
+// so the halves are read from the packed register (op_sel) rather than
+// converted again.
+__device__ __forceinline__ uint32_t residual_pair(uint32_t hi, float e0, float e1, float neg_one) {
+    const f16x2 h = __builtin_bit_cast(f16x2, hi);
+    const f16x2 lo = {static_cast<_Float16>(__builtin_fmaf(static_cast<float>(h.x), neg_one, e0)),
+                      static_cast<_Float16>(__builtin_fmaf(static_cast<float>(h.y), neg_one, e1))};
+    return __builtin_bit_cast(uint32_t, lo);
+}
 
 template <int K, bool FP8, typename OutT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
@@ -189,6 +204,8 @@ void decode_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t total_block
         hsg[h] = (hr[2 * h] < 0.f ? 0x8000u : 0u) | (hr[2 * h + 1] < 0.f ? 0x80000000u : 0u);
 #pragma unroll
     for (int h = 0; h < 2; ++h) asm volatile("" : "+v"(hsg[h]));
+    float neg_one = -1.0f;
+    asm volatile("" : "+v"(neg_one));
     // Keep the operand constants in registers instead of recomputing them in the loop.
 #pragma unroll
     for (int r = 0; r < 8; ++r) asm volatile("" : "+v"(bl[r]));
@@ -308,22 +325,23 @@ void decode_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t total_block
                 const int a = rd * kTilesPerRound + t;
                 f32x4 d = {0.f, 0.f, 0.f, 0.f};
                 if constexpr (FP8) {
-                    // exact split: hi keeps the top 11 significant bits (low 13 mantissa bits cleared),
-                    // lo = e - hi has at most 11 (e is a multiple of 2^-9 below 2^13)
-                    f16x8 bv;
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const float ev = e[a][q];
-                        const float hi32 = __uint_as_float(__float_as_uint(ev) & 0xFFFFE000u);
-                        bv[q] = static_cast<_Float16>(hi32);
-                        bv[q + 4] = static_cast<_Float16>(ev - hi32);
-                    }
-                    // A rows: +-sv of the output column (sign bits from H16 via XOR)
-                    const uint32_t a01 = sv2[a] ^ hsg[0], a23 = sv2[a] ^ hsg[1];
-                    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-                    const u32x4v araw = {a01, a23, a01, a23};
-                    const f16x8 avh = __builtin_bit_cast(f16x8, araw);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(avh, bv, d, 0, 0, 0);
+                    // exact split: hi = e rounded to fp16 (11 significant bits), lo = e - hi, formed by a
+                    // mixed-precision fma straight into fp16.  e is a multiple of 2^-9 below 2^13, so
+                    // |lo| <= ulp(hi) / 2 is a multiple of 2^-9 with at most 11 significant bits: exact.
+                    uint32_t hi01 = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(e[a][0]),
+                                                                              static_cast<_Float16>(e[a][1])});
+                    uint32_t hi23 = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(e[a][2]),
+                                                                              static_cast<_Float16>(e[a][3])});
+                    asm volatile("" : "+v"(hi01), "+v"(hi23));
+                    typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+                    const u32x2v hraw = {hi01, hi23};
+                    const u32x2v lraw = {residual_pair(hi01, e[a][0], e[a][1], neg_one), residual_pair(hi23, e[a][2], e[a][3], neg_one)};
+                    // A rows: +-sv of the output column (sign bits from H16 via XOR), shared by the hi and lo
+                    // products (k = the lane group's four columns 4 g .. 4 g + 3)
+                    const u32x2v araw = {sv2[a] ^ hsg[0], sv2[a] ^ hsg[1]};
+                    const f16x4 avh = __builtin_bit_cast(f16x4, araw);
+                    d = __builtin_amdgcn_mfma_f32_16x16x16f16(avh, __builtin_bit_cast(f16x4, hraw), d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x16f16(avh, __builtin_bit_cast(f16x4, lraw), d, 0, 0, 0);
                 } else {
 #pragma unroll
                     for (int q = 0; q < 4; ++q)
