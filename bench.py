@@ -41,6 +41,10 @@ FP32_PEAK_TFLOPS = 157.3
 VITERBI_HBM_BYTES_PER_TILE = 1.629e6
 # Same counters for the decode launches: 1.013 x their algorithmic bytes (profiles/decode_kernel_layer.md).
 DECODE_TRAFFIC_OVER_ALGORITHMIC = 1.013
+# Same counters at the bench's GEMM and Hadamard shapes (profiles/gemm_tn_kernels_expert_shapes.md,
+# profiles/hadamard_kernel_expert_matrix.md): HBM bytes per launch.
+GEMM_HBM_BYTES = {"hessian_capture": 2.415e9, "ldlq_span_update": 1.485e8}
+HADAMARD_HBM_BYTES = {"left": 1.1782e8, "right": 1.1765e8}
 
 
 def log(msg: str) -> None:
@@ -465,17 +469,17 @@ def gemm_bench(steps: int = 5):
     del L, W, Q, P
     torch.cuda.empty_cache()
 
-    def line(name, ms, fl, dtype, shape, what):
+    def line(key, name, ms, fl, dtype, shape, what):
         t = fl / (ms / 1e3) / 1e12
         return {"kernel": name, "shape": shape, "ms": round(ms, 4), "roofline": {
             "bound": "mfma", "achieved": round(t, 1), "peak": MFMA_PEAK_TFLOPS[dtype], "unit": "TFLOP/s",
-            "frac": round(t / MFMA_PEAK_TFLOPS[dtype], 4), "traffic": None,
+            "frac": round(t / MFMA_PEAK_TFLOPS[dtype], 4), "traffic": round(GEMM_HBM_BYTES[key]),
             "algorithmic": f"{what} = {fl:.4g} flops/launch ({dtype} in, f32 accumulate)"}}
 
     return {
-        "hessian_capture": line("gemm_tn_bf16_kernel", ms_h, fl_h, "bf16", f"X [{n} x {k}] bf16 -> H [{k} x {k}] f32",
-                                "n k (k + 1) (symmetric)"),
-        "ldlq_span_update": line("gemm_tn_f32_kernel", ms_l, fl_l, "f32",
+        "hessian_capture": line("hessian_capture", "gemm_tn_bf16_kernel", ms_h, fl_h, "bf16",
+                                f"X [{n} x {k}] bf16 -> H [{k} x {k}] f32", "n k (k + 1) (symmetric)"),
+        "ldlq_span_update": line("ldlq_span_update", "gemm_tn_f32_kernel", ms_l, fl_l, "f32",
                                  f"L^T [{m} x {kk}] (W - Q) [{kk} x {nn}] f32", "2 M N K"),
     }
 
@@ -499,7 +503,7 @@ def hadamard_bench(steps: int = 5):
         gbps = 8.0 * k * n / (ms / 1e3) / 1e9
         out[side] = {"kernel": "hadamard_kernel", "ms": round(ms, 4), "roofline": {
             "bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-            "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+            "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": round(HADAMARD_HBM_BYTES[side]),
             "algorithmic": f"8 B/element x {k * n} elements/launch"}}
     del W
     torch.cuda.empty_cache()
