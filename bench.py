@@ -36,6 +36,9 @@ CONTEXT = 128
 EDGES_PER_WEIGHT = (256 + 2 * CONTEXT) / 256 * 65536  # 131,072 at C=128
 FLOPS_PER_EDGE = 3  # d = label - x (1), fma(d, d, cost) (2)
 FP32_PEAK_TFLOPS = 157.3
+FP32_UNPACKED_PEAK_TFLOPS = 78.6  # 256 CUs x 64 FP32 FMA lanes x 2 flops x 2.4 GHz, no packed FP32
+# VALU issue-slot occupancy of viterbi_tiles_kernel by PMC (K3, K2; profiles/viterbi_tiles_kernel_microbench.md)
+VITERBI_VALU_ISSUE_FRAC_PMC = {"K2": 1.06, "K3": 0.94}
 # HBM bytes per tile of the Viterbi kernel (FETCH_SIZE x 2.00 + WRITE_SIZE x 1.00 per dispatch, calibrated on a
 # 4 GiB device copy; profiles/viterbi_tiles_kernel_microbench.md): mostly the traceback decision stream.
 VITERBI_HBM_BYTES_PER_TILE = 1.629e6
@@ -625,6 +628,12 @@ def main() -> int:
             "traffic": round(VITERBI_HBM_BYTES_PER_TILE * args.tiles),
             "kernel": "viterbi_tiles_kernel",
             "algorithmic": f"{FLOPS_PER_EDGE} FP32 flops/edge x {int(EDGES_PER_WEIGHT)} edges/weight x {weights_per_k} weights/launch",
+            # The 157.3 TFLOP/s peak counts packed FP32; this build disables packed FP32 ops, which halves the
+            # vector ceiling.  PMC on the same kernel puts VALU issue at 94-106% of slots (K2 above 1: its compares
+            # into SGPR masks retire in fewer than 4 cycles).
+            "peak_without_packed_fp32": FP32_UNPACKED_PEAK_TFLOPS,
+            "frac_without_packed_fp32": round(achieved / FP32_UNPACKED_PEAK_TFLOPS, 4),
+            "valu_issue_frac_pmc": VITERBI_VALU_ISSUE_FRAC_PMC,
         },
     }
     if not args.no_cpu_baseline:
