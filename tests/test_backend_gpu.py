@@ -173,6 +173,32 @@ def test_quantize_qsrt_end_to_end_small(bits):
     assert err < (0.5 if bits == 2 else 0.3)
 
 
+def test_factored_hessian_stays_on_the_device():
+    """The conditioned Hessian and its block-LDL factor stay in HBM after
+    finalisation (no host round trip); refactoring the kept Hessian gives the
+    stored factor back, and a second matrix on the same Hessian reuses it."""
+
+    _say("[backend] factored Hessian residency")
+    k, n = 256, 256
+    x = _ar1(2048, k, 0.8, 50)
+    H = torch.from_numpy(x.T @ x).float()
+    shared = make_shared_h(k, torch.device("cuda:0"), H)
+    shared["count"] = 2048
+    rng = np.random.default_rng(51)
+    W = torch.from_numpy((rng.standard_normal((k, n)) * 0.02).astype(np.float32)).cuda()
+    qa = _qa(3)
+    _, proxy, _ = be.quantize_qsrt(W.clone(), shared, qa, False)
+    assert shared["H"].is_cuda and shared["L"].is_cuda
+    L_again, H_again = be.block_ldl(shared["H"].clone(), 16, qa, False)
+    d = torch.arange(k)
+    L_again[d, d] = 0
+    assert torch.equal(H_again, shared["H"])
+    assert torch.allclose(L_again, shared["L"], rtol=0, atol=1e-6)
+    L_obj = shared["L"]
+    _, proxy2, _ = be.quantize_qsrt(W.clone(), shared, _qa(3), False)
+    assert shared["L"] is L_obj and proxy2 == pytest.approx(proxy, rel=1e-6)
+
+
 def test_quantize_uniform_batch_shared_hessian_matches_single():
     _say("[backend] quantize_uniform_batch shared H")
     k, n = 256, 256
