@@ -12,6 +12,11 @@
   the payload closes, decodes to the encoder's reconstruction, carries
   exactly K bits per weight, and sampled tile-quantizer calls replay
   bit-exact on the CPU oracle.
+* Layer decode records (config 5): a gate-shaped [7168 x 2048] payload with
+  its 16 records along N and a down-shaped [2048 x 7168] one with them along
+  K, 14 K3 + 2 K4 records each, decoded through one prepared plan; sampled
+  128-row block rows match the float64 oracle (the decode is separable by
+  block rows).
 """
 
 from __future__ import annotations
@@ -22,8 +27,10 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import fmt as ofmt
 from oracle import tables as otables
 from oracle import viterbi as ov
+from qsrt_amd import decode as D
 from qsrt_amd import exl3_encoder_backend as be
 from qsrt_amd import qsrt as Q
 from qsrt_amd.exl3_reference import decode_regularized_weight, reconstruct_trellis_states
@@ -134,3 +141,67 @@ def test_kimi_matrix_full_size_encode_closes_and_replays(monkeypatch):
         o_recon, o_states = ov.encode(tiles, otables.t12_values(bits), K=bits, context=128, boundary_lag=lag)
         assert np.array_equal(st.view(np.uint16), o_states), f"call {i}"
         assert np.array_equal(recon, o_recon), f"call {i}"
+
+
+LAYER_RECORD_BITS = (3,) * 14 + (4,) * 2  # config 5: 14 K3 + 2 K4 records per matrix
+
+
+def _record_payload(rbits, rate_axis, other_tiles, seed):
+    """Record-major words of random closed paths, one record (8 rate-axis
+    tiles) per entry of ``rbits``; returns (states [kt, nt, 256], words)."""
+
+    g = torch.Generator().manual_seed(seed)
+    shape = (8 * len(rbits), other_tiles) if rate_axis == "k" else (other_tiles, 8 * len(rbits))
+    states = torch.empty((*shape, 256), dtype=torch.int16)
+    pieces = []
+    for i, bits in enumerate(rbits):
+        e = torch.randint(0, 1 << bits, (8, other_tiles, 256) if rate_axis == "k" else (other_tiles, 8, 256),
+                          generator=g)
+        st = reconstruct_trellis_states(e, bits)
+        if rate_axis == "k":
+            states[8 * i:8 * i + 8] = st
+        else:
+            states[:, 8 * i:8 * i + 8] = st
+        pieces.append(Q.pack_trellis_edges(st.reshape(-1, 256), bits).reshape(-1))
+    return states, torch.cat(pieces)
+
+
+def test_layer_records_full_size_decode_matches_oracle():
+    _say("[full] decode plan: gate [7168 x 2048] records along N, down [2048 x 7168] records along K")
+    luts = {b: sqg_xor_cheb_t12_bytes(b).to(DEV) for b in set(LAYER_RECORD_BITS)}
+    cases = [("n", 448, 61), ("k", 448, 62)]
+    payloads, meta = [], []
+    for axis, other, seed in cases:
+        states, words = _record_payload(LAYER_RECORD_BITS, axis, other, seed)
+        kt, nt = states.shape[:2]
+        g = torch.Generator().manual_seed(seed + 100)
+        suh = (torch.rand(16 * kt, generator=g) + 0.5).half()
+        svh = (torch.rand(16 * nt, generator=g) - 0.5).half()
+        out = torch.empty((16 * kt, 16 * nt), dtype=torch.float32, device=DEV)
+        payloads.append((words.to(DEV), LAYER_RECORD_BITS, axis, (suh.float() / 128).to(DEV), svh.float().to(DEV),
+                         out))
+        meta.append((states, suh, svh, axis))
+    plan = D.DecodePlan.for_records(payloads, luts, out_dtype=torch.float32)
+    plan.run()
+    torch.cuda.synchronize()
+    for (states, suh, svh, axis), p in zip(meta, payloads):
+        st = states.numpy().view(np.uint16)
+        kt, nt = st.shape[:2]
+        record = np.empty((kt, nt), dtype=np.int64)  # rate of every tile
+        for i, bits in enumerate(LAYER_RECORD_BITS):
+            if axis == "k":
+                record[8 * i:8 * i + 8] = bits
+            else:
+                record[:, 8 * i:8 * i + 8] = bits
+        tables = {b: otables.t12_values(b) for b in set(LAYER_RECORD_BITS)}
+        got = p[5].cpu().double().numpy()
+        rows = np.random.default_rng(len(axis) + kt).choice(kt // 8, size=4, replace=False)
+        for br in sorted(rows.tolist()):
+            sl = slice(8 * br, 8 * br + 8)
+            labels = np.empty((8, nt, 256), dtype=np.float64)
+            for b, table in tables.items():
+                mask = record[sl] == b
+                labels[mask] = table[st[sl][mask]]
+            want = ofmt.decode_tile_values(labels, suh.float().numpy()[128 * br:128 * br + 128], svh.float().numpy())
+            block = got[128 * br:128 * br + 128]
+            assert np.max(np.abs(block - want)) <= 2e-6 * np.abs(want).max(), f"{axis} block row {br}"
