@@ -235,36 +235,46 @@ def layer_encode_bench(sample: int = 8, batch: int = 8, rho: float = 0.85):
         return _qsrt_quant_args(plan, matrix=matrix, layer=24, device=dev, shared_scale_scope=scope,
                                 transform_seeds=default_qsrt_transform_seeds(24, matrix))
 
-    proxies = []
-    t0 = time.perf_counter()
-    for g0 in range(0, sample, batch):
-        group = experts[g0:g0 + batch]
-        weights, hs, qas = [], [], []
-        for item in group:
-            g_c, u_c, _ = item["c"]
-            for name, m in (("w1", g_c), ("w3", u_c)):
-                shared = make_shared_h(hidden, dev, item["h13"])
+    def run_sample():
+        proxies = []
+        for g0 in range(0, sample, batch):
+            group = experts[g0:g0 + batch]
+            weights, hs, qas = [], [], []
+            for item in group:
+                g_c, u_c, _ = item["c"]
+                for name, m in (("w1", g_c), ("w3", u_c)):
+                    shared = make_shared_h(hidden, dev, item["h13"])
+                    shared["count"] = item["tokens"]
+                    weights.append(m.T.contiguous())
+                    hs.append(shared)
+                    qas.append([qa(name, "n", ("layer-bench", g0))])
+            up = be.quantize_qsrt_batch(weights, hs, qas)
+            weights, hs, qas = [], [], []
+            for i, item in enumerate(group):
+                g_c, u_c, d_c = item["c"]
+                g_hat, u_hat = up[2 * i][0]["weight_q"].T, up[2 * i + 1][0]["weight_q"].T
+                gs, us, _ = decode_coupled_weights((g_hat, u_hat, d_c), spec)
+                x = item["x"]
+                h = (torch.nn.functional.silu(x @ gs.T) * (x @ us.T)).contiguous()
+                h2 = item["ex"].transform_h2(gemm.gram_(torch.zeros((inter, inter), device=dev), h, 1.0 / x.shape[0]))
+                shared = make_shared_h(inter, dev, h2)
                 shared["count"] = item["tokens"]
-                weights.append(m.T.contiguous())
+                weights.append(d_c.T.contiguous())
                 hs.append(shared)
-                qas.append([qa(name, "n", ("layer-bench", g0))])
-        up = be.quantize_qsrt_batch(weights, hs, qas)
-        weights, hs, qas = [], [], []
-        for i, item in enumerate(group):
-            g_c, u_c, d_c = item["c"]
-            g_hat, u_hat = up[2 * i][0]["weight_q"].T, up[2 * i + 1][0]["weight_q"].T
-            gs, us, _ = decode_coupled_weights((g_hat, u_hat, d_c), spec)
-            x = item["x"]
-            h = (torch.nn.functional.silu(x @ gs.T) * (x @ us.T)).contiguous()
-            h2 = item["ex"].transform_h2(gemm.gram_(torch.zeros((inter, inter), device=dev), h, 1.0 / x.shape[0]))
-            shared = make_shared_h(inter, dev, h2)
-            shared["count"] = item["tokens"]
-            weights.append(d_c.T.contiguous())
-            hs.append(shared)
-            qas.append([qa("w2", "k", ("layer-bench", g0))])
-        down = be.quantize_qsrt_batch(weights, hs, qas)
-        proxies += [r[0]["proxy"] for r in up] + [r[0]["proxy"] for r in down]
-    torch.cuda.synchronize()
+                qas.append([qa("w2", "k", ("layer-bench", g0))])
+            down = be.quantize_qsrt_batch(weights, hs, qas)
+            proxies += [r[0]["proxy"] for r in up] + [r[0]["proxy"] for r in down]
+        torch.cuda.synchronize()
+        return proxies
+
+    # The first pass pays one-time costs (library code objects loaded on first use of each kernel and shape,
+    # allocator growth); a whole layer pays them once, so the layer time is the cold pass plus the warm
+    # pass's time for every further batch of the same shape.
+    t0 = time.perf_counter()
+    run_sample()
+    cold = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    proxies = run_sample()
     seconds = time.perf_counter() - t0
     weights_per_expert = 3 * hidden * inter
     return {
@@ -274,8 +284,9 @@ def layer_encode_bench(sample: int = 8, batch: int = 8, rho: float = 0.85):
         "sample_experts": chosen,
         "sample_tokens": [item["tokens"] for item in experts],
         "sample_seconds": round(seconds, 3),
+        "sample_seconds_cold": round(cold, 3),
         "M_weights_per_s": round(sample * weights_per_expert / seconds / 1e6, 2),
-        "layer_seconds_extrapolated": round(seconds * LAYER_EXPERTS / sample, 1),
+        "layer_seconds_extrapolated": round(cold + seconds * (LAYER_EXPERTS / sample - 1), 1),
         "proxy_err_mean": round(sum(proxies) / len(proxies), 5),
     }
 
