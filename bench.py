@@ -552,8 +552,9 @@ def main() -> int:
                     help="only run a device copy of BYTES (reference for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one MI355X: the encoder hot path is a single-GPU kernel here; "
-              "multi-GPU sharding is design-only (see DESIGN.md)", file=sys.stderr)
+        print("bench.py measures one MI355X: this build runs the encoder on one GPU and does not shard it "
+              "across GPUs (experts would shard with no exchange; see the repository's design notes)",
+              file=sys.stderr)
         return 2
 
     if args.copy_calibration:
