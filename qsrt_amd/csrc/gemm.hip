@@ -87,11 +87,27 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_f32_kernel(float* __restrict
     const int64_t m0 = (blockIdx.x / tiles_n) * kBM, n0 = (blockIdx.x % tiles_n) * kBN;
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
 
+    // With alpha == 1 (the BlockLDLQ products) the accumulators start from C: its reads are issued with the
+    // first operand chunk instead of after the last MFMA, and the epilogue is a plain store.
+    const bool seed = alpha == 1.0f;
     f32x4 acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (seed) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t row = m0 + wm + 16 * i + 4 * g + r;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int64_t col = n0 + wn + 16 * j + c;
+                    if (row < M && col < N) acc[i][j][r] = C[row * ldc + col];
+                }
+            }
+    }
 
     F32Chunk ch;
     load_f32(ch, A, B, B2, 0, m0, n0, M, N, K, lda, ldb, t);
@@ -126,7 +142,12 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_f32_kernel(float* __restrict
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int64_t col = n0 + wn + 16 * j + c;
-                if (col < N) C[row * ldc + col] += alpha * acc[i][j][r];
+                if (col < N) {
+                    if (seed)
+                        C[row * ldc + col] = acc[i][j][r];
+                    else
+                        C[row * ldc + col] += alpha * acc[i][j][r];
+                }
             }
         }
 }
