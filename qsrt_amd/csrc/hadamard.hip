@@ -14,7 +14,7 @@
 // of regularize; the `H *= su` congruence; the `* su`, `* sv` of decode).
 //
 // Design: one 256-thread workgroup per 8192-element tile (block x 8192/block
-// of the two axes).  The tile is read with coalesced float4 loads into LDS,
+// of the two axes; 16384 for block 512 along rows).  The tile is read with coalesced float4 loads into LDS,
 // transformed in two in-register rounds (bits 0..4 of the transformed
 // index, then the remaining bits), each thread owning one 32- or
 // 2^(log2(block)-5)-point line per round, and written back with float4
@@ -25,8 +25,14 @@
 
 namespace {
 
-constexpr int kTileElems = 8192;
 constexpr int kThreads = 256;
+
+// Elements per tile: B x (elements / B).  Block 512 along rows gets twice the usual 8192 so that each row
+// segment it reads and writes is 128 bytes (32 floats) rather than 64.
+template <int NB, bool LEFT>
+constexpr int tile_elems() {
+    return (LEFT && NB == 9) ? 16384 : 8192;
+}
 
 template <int NB>
 __device__ __forceinline__ void fwht(float (&v)[1 << NB]) {
@@ -47,7 +53,7 @@ __device__ __forceinline__ void fwht(float (&v)[1 << NB]) {
 template <int NB, int LO, int NBITS, int S, int O>
 __device__ __forceinline__ void lds_round(float* lds, int t) {
     constexpr int V = 1 << NBITS;
-    constexpr int kLines = kTileElems / V;
+    constexpr int kLines = (O << NB) / V;  // tile elements / V
     static_assert(kLines % kThreads == 0, "line count must fill the workgroup");
 #pragma unroll
     for (int k = 0; k < kLines / kThreads; ++k) {
@@ -70,6 +76,7 @@ __global__ __launch_bounds__(kThreads) void hadamard_kernel(float* __restrict__ 
                                                             const float* __restrict__ pre_mul,
                                                             const float* __restrict__ pre_div,
                                                             const float* __restrict__ post_mul, float norm) {
+    constexpr int kTileElems = tile_elems<NB, LEFT>();
     constexpr int B = 1 << NB;        // transformed extent of one tile
     constexpr int O = kTileElems / B;  // other-axis extent of one tile
     constexpr int S = O + 1;           // LDS stride per transformed index (odd: spreads banks)
@@ -165,7 +172,7 @@ template <int NB>
 int launch(float* x, int64_t rows, int64_t cols, int64_t ld, int side, const float* pre_mul, const float* pre_div,
            const float* post_mul, hipStream_t stream) {
     constexpr int B = 1 << NB;
-    constexpr int O = kTileElems / B;
+    const int O = (side == 0 ? tile_elems<NB, true>() : tile_elems<NB, false>()) / B;
     const int64_t ext_a = side == 0 ? rows : cols;
     const int64_t ext_b = side == 0 ? cols : rows;
     const int64_t tiles_b = (ext_b + O - 1) / O;
