@@ -11,9 +11,15 @@ Restates ``qsrt/exl3_encoder_backend.py``:
   T - Q == (I + L0^T)(W - Q) for an arbitrary quantizer
   (``tests/test_blockldlq_proof.py:62-95``) and by a direct per-block loop;
 * ``regularize`` (:2580-2708) up to the global-scale search and the
-  Hessian congruence of ``_factor_capture_H`` (:2125-2160) -- "parity
-  unpinned" beyond these restatements: no reference test or fixture holds
-  values for them (the reference backend cannot be imported here).
+  Hessian congruence of ``_factor_capture_H`` (:2125-2160): no reference
+  test or fixture holds values for them (the reference backend cannot be
+  imported here).  They are pinned by the mathematics instead: the
+  congruence equals T H T^T with T = (I (x) H_128) D_su built densely from
+  scipy's Sylvester Hadamard, keeps H's spectrum and fixes I; the
+  regularisation is inverted exactly by the decoder's formula, gives every
+  128-row block an RMS of g * 1.24371088, and returns
+  su = -su rms_rows(W) / (1.24371088 g) in closed form.  The constant
+  1.24371088 itself is the reference's (:2580-2708).
 """
 
 from __future__ import annotations

@@ -105,3 +105,58 @@ def test_fallback_hessian_marks_q_fallback():
     shared["count"] = 0
     q_fallback, *_ = be.finalize_capture_H(shared, {"seed": 3}, False)
     assert q_fallback and shared["L"] is None
+
+
+def _block_had_signs(k, signs):
+    """Dense T = (I_{k/128} (x) H_128 / sqrt(128)) D_signs, built with scipy's Sylvester Hadamard."""
+
+    import scipy.linalg
+
+    h = scipy.linalg.hadamard(128) / np.sqrt(128.0)
+    return np.kron(np.eye(k // 128), h) @ np.diag(np.asarray(signs, dtype=np.float64).reshape(-1))
+
+
+def test_oracle_congruence_pinned_by_dense_construction_and_invariants():
+    # congruence is an orthogonal similarity T H T^T: a one-sided sign, a transposed or unnormalised
+    # Hadamard, or a row-only transform fails the dense product, the spectrum or the round trip
+    k = 256
+    rng = np.random.default_rng(11)
+    H = _spd(k, 12)
+    s = np.sign(rng.standard_normal(k))
+    T = _block_had_signs(k, s)
+    got = oldlq.congruence(H, s)
+    assert np.allclose(got, T @ H @ T.T, atol=1e-12)
+    assert np.allclose(got, got.T, atol=1e-12)
+    assert np.allclose(np.linalg.eigvalsh(got), np.linalg.eigvalsh(H), atol=1e-10)
+    assert np.allclose(oldlq.congruence(np.eye(k), s), np.eye(k), atol=1e-12)
+    ones = np.ones(k)
+    assert np.allclose(oldlq.congruence(oldlq.congruence(H, ones), ones), H, atol=1e-12)  # H_128 is an involution
+
+
+def test_oracle_regularize_pinned_by_inverse_and_closed_forms():
+    # W' = g H_L diag(1/su') (W diag(1/sv) H_R) with su' = su rms / -c; the decoder's inverse
+    # W = diag(sv)-scaled ((su_out * (H_L^T W')) H_R^T) must return W, each 128-row block of W' has RMS g c
+    # (H_L is orthogonal within the block), and su_out = -su rms_rows(W) / (c g) with rms_rows unchanged by
+    # the orthogonal H_R
+    k, n, g = 256, 384, 0.8
+    rng = np.random.default_rng(13)
+    W = rng.standard_t(5, size=(k, n)) * 0.02
+    W[7] = 0.0  # a zero row takes the reference's rms = 0.1 substitute
+    su = np.sign(rng.standard_normal(k))
+    sv = np.sign(rng.standard_normal(n))
+    Wr, su_out, sv_out = oldlq.regularize(W, su, sv, g)
+    c = oldlq.CODEBOOK_SCALE
+    TL = _block_had_signs(k, np.ones(k))
+    TR = _block_had_signs(n, np.ones(n))
+    back = ((su_out.reshape(k, 1) * (TL.T @ Wr)) @ TR.T) * sv_out.reshape(1, n)
+    assert np.allclose(back, W, atol=1e-12)
+    rms = np.sqrt((W * W).mean(axis=1))
+    rms[7] = 0.1
+    assert np.allclose(su_out.reshape(-1), (-su * rms / c + 1e-10) / g, rtol=1e-12)
+    nonzero = np.ones(k, dtype=bool)
+    nonzero[7] = False
+    for b in range(k // 128):
+        rows = slice(128 * b, 128 * b + 128)
+        if nonzero[rows].all():
+            assert np.isclose(np.sqrt(np.mean(Wr[rows] ** 2)), g * c, rtol=1e-8)
+    assert np.array_equal(sv_out.reshape(-1), sv)
