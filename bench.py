@@ -84,6 +84,71 @@ def ar1_rows(n: int, k: int, rho: float, gen: torch.Generator, device) -> torch.
     return (z.double() @ T).float()
 
 
+def student_t_like(shape, *, nu: int = 5, std: float, gen: torch.Generator) -> torch.Tensor:
+    """Student-t(nu) scaled to standard deviation ``std``, drawn on the
+    generator's device: ``z / sqrt(chi2_nu / nu)`` with the chi-square a sum
+    of ``nu`` squared normals."""
+
+    dev = gen.device
+    z = torch.randn(shape, generator=gen, device=dev)
+    chi2 = torch.zeros(shape, device=dev)
+    for _ in range(nu):
+        chi2.addcmul_(u := torch.randn(shape, generator=gen, device=dev), u)
+    return z.div_(chi2.div_(nu).sqrt_()).mul_(std / math.sqrt(nu / (nu - 2.0)))
+
+
+def ar1_scan(n: int, k: int, rho: float, gen: torch.Generator, *, block: int = 128) -> torch.Tensor:
+    """``n`` rows of the AR(1) process along channels (x_0 = z_0,
+    x_j = rho x_{j-1} + sqrt(1 - rho^2) z_j, so Sigma_ij = rho^|i-j|), FP32 on
+    the generator's device: each block of ``block`` channels is one
+    triangular product, then the carries run across the blocks."""
+
+    dev = gen.device
+    if k % block:
+        raise ValueError("channels must be a multiple of the scan block")
+    c = math.sqrt(1.0 - rho * rho)
+    z = torch.randn((n, k), generator=gen, device=dev)
+    z[:, 0] /= c  # x_0 = z_0: the first channel's innovation has weight 1, not c
+    i = torch.arange(block, device=dev, dtype=torch.float64)
+    gap = i[None, :] - i[:, None]
+    T = torch.where(gap >= 0, c * rho ** gap.clamp(min=0), torch.zeros((), dtype=torch.float64, device=dev)).float()
+    x = (z.view(n, k // block, block) @ T).contiguous()
+    carry = (rho ** (i + 1)).float()
+    for b in range(1, k // block):
+        x[:, b].addcmul_(x[:, b - 1, -1:], carry[None, :])
+    return x.view(n, k)
+
+
+def config_expert(cfg: int, device, *, expert: int = 0, tokens: int | None = None) -> dict:
+    """Seeded synthetic inputs of BASELINE configs 1, 3, 4 and 5 (one expert):
+    weights ``w_gate, w_up [inter, hidden]``, ``w_down [hidden, inter]`` and
+    calibration rows ``x [tokens, hidden]``.
+
+    cfg 1: hidden 256, inter 512, FP32 weights t5 x 0.02, 4096 rows rho 0.8.
+    cfg 3: hidden 5120, inter 1536, bf16 weights t5 x 0.015, 8192 rows
+           rho 0.9, 8 seeded outlier channels at 20x variance.
+    cfg 4: hidden 7168, inter 2048, bf16 weights t5 x 0.015, 16384 rows rho 0.85.
+    cfg 5: the cfg-4 shape, one generator per expert, ``tokens`` routed rows.
+    """
+
+    shapes = {1: (256, 512, 4096, 0.8, 0.02, False), 3: (5120, 1536, 8192, 0.9, 0.015, True),
+              4: (7168, 2048, 16384, 0.85, 0.015, True), 5: (7168, 2048, 0, 0.85, 0.015, True)}
+    hidden, inter, n, rho, std, bf16 = shapes[cfg]
+    n = n if tokens is None else tokens
+    gen = torch.Generator(device=device).manual_seed((20261201 + cfg) * 1000 + expert)
+    w = []
+    for shape in ((inter, hidden), (inter, hidden), (hidden, inter)):
+        t = student_t_like(shape, std=std, gen=gen)
+        w.append(t.bfloat16().float() if bf16 else t)
+    x = ar1_scan(max(n, 1), hidden, rho, gen)[:n]
+    outliers = None
+    if cfg == 3:
+        outliers = torch.randperm(hidden, generator=gen, device=device)[:8].sort().values
+        x[:, outliers] *= math.sqrt(20.0)
+    return {"w_gate": w[0], "w_up": w[1], "w_down": w[2], "x": x, "hidden": hidden, "inter": inter,
+            "outliers": outliers}
+
+
 def run_expert_encode(bits: int = 3, hidden: int = 7168, inter: int = 2048, tokens: int = 16384, rho: float = 0.85, log=print):
     """BASELINE config 4 at rate ``bits``: one Kimi-class SwiGLU expert in the
     exact coupled basis (qsrt_amd.qsrt_coupled, draw 0), H13 = X^T X from

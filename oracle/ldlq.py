@@ -90,23 +90,47 @@ def congruence(H: np.ndarray, su_signs: np.ndarray) -> np.ndarray:
     return np.einsum("kbj,ji->kbi", M.reshape(k, k // 128, 128), h).reshape(k, k)
 
 
-def regularize(weight: np.ndarray, su_signs: np.ndarray, sv_signs: np.ndarray, g_scale: float):
+def regularize(weight: np.ndarray, su_signs: np.ndarray, sv_signs: np.ndarray, g_scale: float, *,
+               g_into_sv: bool = False, input_scales: np.ndarray | None = None):
     """Regularisation with apply_out_scales=False and a fixed global scale:
     W /= sv; W <- W Had; su = su * rms_rows(W) / -1.24371088 + 1e-10;
-    W /= su; W <- Had W; W *= g; su /= g.  Returns (W, su, sv) in float64."""
+    W /= su; W <- Had W; W *= g; su /= g (sv /= g with ``g_into_sv``, as
+    ``g_scale_into_sv`` does for w1/w3, :2727-2751).  ``input_scales``
+    replaces rms_rows(W) by a layer-shared profile (the reference's
+    ``shared_input_scales_key``, :2669-2672).  Returns (W, su, sv) in
+    float64."""
 
     W = np.asarray(weight, dtype=np.float64).copy()
     k, n = W.shape
-    sv = np.asarray(sv_signs, dtype=np.float64).reshape(1, n)
+    sv = np.asarray(sv_signs, dtype=np.float64).reshape(1, n).copy()
     su = np.asarray(su_signs, dtype=np.float64).reshape(k, 1)
     h = hadamard(128)
     W /= sv
     W = np.einsum("kbj,ji->kbi", W.reshape(k, n // 128, 128), h).reshape(k, n)
-    rms = np.sqrt((W * W).mean(axis=1, keepdims=True))
-    rms[np.abs(rms) < 1e-30] = 0.1
+    if input_scales is None:
+        rms = np.sqrt((W * W).mean(axis=1, keepdims=True))
+        rms[np.abs(rms) < 1e-30] = 0.1
+    else:
+        rms = np.asarray(input_scales, dtype=np.float64).reshape(k, 1)
     su = su * rms / (-CODEBOOK_SCALE) + 1e-10
     W /= su
     W = np.einsum("ij,bjn->bin", h, W.reshape(k // 128, 128, n)).reshape(k, n)
     W *= g_scale
-    su = su / g_scale
+    if g_into_sv:
+        sv = sv / g_scale
+    else:
+        su = su / g_scale
     return W, su, sv
+
+
+def input_rms(weight: np.ndarray, sv_signs: np.ndarray) -> np.ndarray:
+    """rms_rows(W / sv @ Had): the input-channel profile ``regularize``
+    derives (and a layer-shared key reuses)."""
+
+    W = np.asarray(weight, dtype=np.float64)
+    k, n = W.shape
+    W = W / np.asarray(sv_signs, dtype=np.float64).reshape(1, n)
+    W = np.einsum("kbj,ji->kbi", W.reshape(k, n // 128, 128), hadamard(128)).reshape(k, n)
+    rms = np.sqrt((W * W).mean(axis=1, keepdims=True))
+    rms[np.abs(rms) < 1e-30] = 0.1
+    return rms

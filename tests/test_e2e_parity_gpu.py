@@ -1,0 +1,138 @@
+"""End-to-end payload parity: ``quantize_qsrt`` on the GPU against an
+untethered CPU encode (``oracle.encode``) on the same seeded inputs.
+
+The CPU side receives only what the GPU side receives -- the weight, the
+captured ``X^T X`` sum and its count, the seeds -- plus the global scale the
+GPU's search picked (that search is pinned on its own in
+``test_gscale_gpu.py``).  It then runs the float64 Hessian preparation,
+congruence, block LDL, regularisation and BlockLDLQ with the C oracle
+Viterbi on every 16-row block.  Nothing of the GPU run feeds the CPU
+recursion.
+
+Bars: packed words equal byte for byte wherever the
+paths agree; a tile whose path differs while every tile below it in its
+column agrees saw the same target up to FP32 rounding, so it is a near-tie
+resolved the other way, and its squared error must be within 1e-6 relative
+of the CPU path's on the CPU target.  The tile mismatch rate is printed.
+Tiles above such a tile in the same column see a different target (the
+feedback runs along columns), so they are counted but not held to the tie
+bar; their effect is bounded through the proxy error.
+"""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import bench
+from oracle import encode as oenc
+from oracle import fmt as ofmt
+from oracle import tables as otables
+from qsrt_amd import exl3_encoder_backend as be
+from qsrt_amd.ldlq import make_shared_h
+from qsrt_amd.sqg_e4m3 import sqg_xor_cheb_t12_bytes
+from qsrt_amd.transform_seeds import default_qsrt_transform_seeds
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+TIE_SSE_REL = 1e-6
+
+
+def _say(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def _signs(n: int, seed: int) -> np.ndarray:
+    """The reference's sign draw on a CPU generator (qsrt/rng.py:8-20)."""
+
+    g = torch.Generator().manual_seed(int(seed))
+    return (torch.randn(n, generator=g).sign() + 1e-5).sign().double().numpy()
+
+
+def _gpu_encode(W: torch.Tensor, H_sum: torch.Tensor, count: int, bits: int, seeds) -> tuple:
+    shared = make_shared_h(W.shape[0], DEV, H_sum)
+    shared["count"] = count
+    qa = {"K": bits, "seed": seeds.input_sign, "sv_seed": seeds.output_sign, "sigma_reg": 0.01,
+          "devices": [str(DEV)], "apply_out_scales": False, "tailbite_context": 128,
+          "sqg_e4m3_lut": sqg_xor_cheb_t12_bytes(bits)}
+    weight_q, proxy, tensors = be.quantize_qsrt(W.to(DEV).clone(), shared, qa, False)
+    torch.cuda.synchronize()
+    return weight_q, proxy, tensors, qa, shared
+
+
+def _check_matrix(name: str, W: torch.Tensor, H_sum: torch.Tensor, count: int, bits: int, seeds) -> dict:
+    k, n = W.shape
+    _say(f"[e2e] {name}: [{k} x {n}] K{bits} on cuda:0")
+    weight_q, proxy, tensors, qa, shared = _gpu_encode(W, H_sum, count, bits, seeds)
+    trellis = tensors["trellis"].cpu().numpy().view(np.uint16)
+    g_states = ofmt.cyclic_states(ofmt.unpack_symbols(trellis, bits), bits)
+    _say(f"[e2e] {name}: GPU proxy {proxy:.6f}, g_scale {qa['g_scale']:.6f}; CPU encode")
+    labels = {bits: otables.t12_values(bits)}
+    lags = {bits: 0 if bits == 2 else 1}
+    cpu = oenc.encode_matrix(W.double().cpu().numpy(), H_sum.double().cpu().numpy(), count,
+                             _signs(k, seeds.input_sign), _signs(n, seeds.output_sign), qa["g_scale"],
+                             np.full((k // 16, n // 16), bits), labels, lags, sigma_reg=0.01)
+    stats = oenc.compare_states(g_states, cpu, labels, np.full((k // 16, n // 16), bits))
+    words = ofmt.pack_words(cpu["states"], bits)
+    same_tile = ~np.any(g_states != cpu["states"], axis=2)
+    cpu_proxy = oenc.proxy(cpu["W_r"], cpu["Q"], cpu["H_c"])
+    deltas = stats["sse_rel_deltas"]
+    _say(f"[e2e] {name}: {stats['differ']} of {stats['tiles']} tiles differ (mismatch rate "
+         f"{stats['mismatch_rate']:.5f}; {len(stats['first'])} near-tie, {stats['propagated']} downstream), "
+         f"max near-tie SSE delta {max(deltas) if deltas else 0.0:.3e}; proxy GPU {proxy:.6f} CPU {cpu_proxy:.6f}")
+    # words of every agreeing tile are the oracle's, byte for byte
+    assert np.array_equal(trellis[same_tile], words[same_tile])
+    # GPU's factor and conditioned metric against the float64 congruence + block LDL
+    L = shared["L"].double().cpu().numpy()
+    H_c = shared["H"].double().cpu().numpy()
+    h_err = np.max(np.abs(H_c - cpu["H_c"])) / np.abs(cpu["H_c"]).max()
+    l_err = np.max(np.abs(L - cpu["L0"])) / max(np.abs(cpu["L0"]).max(), 1.0)
+    _say(f"[e2e] {name}: conditioned H max rel {h_err:.2e}, L max rel {l_err:.2e}")
+    assert h_err <= 1e-5 and l_err <= 1e-4
+    # the GPU's reconstruction (regularised basis) is its states' labels
+    assert np.array_equal(weight_q.cpu().numpy()[np.kron(same_tile, np.ones((16, 16), bool))],
+                          cpu["Q"].astype(np.float32)[np.kron(same_tile, np.ones((16, 16), bool))])
+    for d in deltas:
+        assert d <= TIE_SSE_REL, f"{name}: a differing tile's SSE is {d:.3e} relative from the CPU path's"
+    assert abs(proxy - cpu_proxy) <= 1e-3 * cpu_proxy
+    assert stats["mismatch_rate"] <= 0.01
+    return stats
+
+
+def test_config1_expert_all_three_matrices_match_cpu_encode():
+    """BASELINE config 1 (hidden 256, inter 512, K2): gate and up under
+    H13 = X^T X, down under H2 from the source SwiGLU activations."""
+
+    d = bench.config_expert(1, torch.device("cpu"))
+    x = d["x"].double()
+    h13 = (x.T @ x).float()
+    h = torch.nn.functional.silu(x @ d["w_gate"].double().T) * (x @ d["w_up"].double().T)
+    h2 = (h.T @ h).float()
+    n_rows = x.shape[0]
+    total = {"tiles": 0, "differ": 0}
+    for matrix, W, H in (("w1", d["w_gate"].T, h13), ("w3", d["w_up"].T, h13), ("w2", d["w_down"].T, h2)):
+        stats = _check_matrix(f"config 1 {matrix}", W.contiguous(), H, n_rows, 2,
+                              default_qsrt_transform_seeds(1, matrix))
+        total["tiles"] += stats["tiles"]
+        total["differ"] += stats["differ"]
+    _say(f"[e2e] config 1 expert: tile mismatch rate {total['differ'] / total['tiles']:.5f} "
+         f"({total['differ']} of {total['tiles']})")
+
+
+def test_config3_strip_matches_cpu_encode():
+    """A 1,024-row strip of the config-3 gate matrix (K3): rows 0..1023 of
+    W^T [5120 x 1536] under the matching 1024 x 1024 block of H13, from 8192
+    AR(1) rows (rho 0.9) whose 8 outlier channels (20x variance) are placed
+    inside the strip."""
+
+    gen = torch.Generator().manual_seed((20261201 + 3) * 1000 + 7)
+    k, n, rows = 1024, 1536, 8192
+    x = bench.ar1_scan(rows, k, 0.9, gen)
+    outliers = torch.randperm(k, generator=gen)[:8]
+    x[:, outliers] *= 20.0 ** 0.5
+    W = bench.student_t_like((n, k), std=0.015, gen=gen).bfloat16().float().T.contiguous()
+    xd = x.double()
+    _check_matrix("config 3 strip", W, (xd.T @ xd).float(), rows, 3, default_qsrt_transform_seeds(1, "w1"))
