@@ -129,7 +129,9 @@ size_t qsrt_decode_workspace_bytes(int n_jobs);
  * (out_dtype 0) or f32 (out_dtype 1):
  *   words -> cyclic 16-bit states -> lut_e4m3[state] -> X (tensor-core
  *   order inside each 16x16 tile) -> row_scale . H128 X H128 . col_scale.
- * `jobs` is a HOST array (copied to `workspace` on `stream`); rows and cols
+ * `jobs` is a HOST array, written into `workspace` by a stream-ordered
+ * upload kernel whose arguments carry the jobs (no host staging buffer, no
+ * allocation; `jobs` may be reused as soon as the call returns); rows and cols
  * multiples of 128; words, out, row_scale and col_scale 16-byte aligned;
  * tile and block strides multiples of 8; out_ld >= cols and a multiple of 8; lut_e4m3
  * 16-byte aligned.  exact_fp8 != 0 selects the FP8 matrix-core path, exact

@@ -385,6 +385,32 @@ void launch(const Job* jobs, int n_jobs, int64_t total, const uint8_t* lut, int 
                            lut);
 }
 
+// Job-table upload by kernel argument: the host validates and converts up to
+// kUploadChunk jobs into a by-value argument, and one small kernel writes them
+// to the device table.  Arguments are captured when the launch is enqueued,
+// so there is no host buffer whose lifetime must outlast an asynchronous
+// copy, no allocation, and the upload is stream-ordered like any launch.
+constexpr int kUploadChunk = 16;
+
+struct JobChunk {
+    Job jobs[kUploadChunk];
+    int count;
+};
+
+__global__ __launch_bounds__(64) void upload_jobs_kernel(JobChunk chunk, Job* __restrict__ dst) {
+    const int i = static_cast<int>(threadIdx.x);
+    if (i < chunk.count) dst[i] = chunk.jobs[i];
+}
+
+bool job_ok(const qsrt_decode_job& s) {
+    return s.words && s.row_scale && s.col_scale && s.out && s.rows >= 0 && s.cols >= 0 && s.rows % 128 == 0 &&
+           s.cols % 128 == 0 && s.out_ld >= s.cols && s.out_ld % 8 == 0 &&
+           reinterpret_cast<uintptr_t>(s.words) % 16 == 0 && s.tile_row_stride % 8 == 0 &&
+           s.tile_col_stride % 8 == 0 && s.block_row_stride % 8 == 0 && s.block_col_stride % 8 == 0 &&
+           reinterpret_cast<uintptr_t>(s.out) % 16 == 0 && reinterpret_cast<uintptr_t>(s.col_scale) % 16 == 0 &&
+           reinterpret_cast<uintptr_t>(s.row_scale) % 16 == 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -407,51 +433,52 @@ int qsrt_decode_prepare(const qsrt_decode_job* jobs, int n_jobs, int K, void* wo
         return qsrt::fail(qsrt::kWorkspaceTooSmall, "decode workspace needs %zu bytes",
                           qsrt_decode_workspace_bytes(n_jobs));
     if (reinterpret_cast<uintptr_t>(workspace) % 16) return qsrt::fail(qsrt::kBadArgument, "workspace must be 16-byte aligned");
-    Job* host = static_cast<Job*>(malloc(sizeof(Job) * n_jobs));
-    if (!host) return qsrt::fail(qsrt::kHipError, "host allocation failed");
-    int64_t total = 0;
-    int kept = 0;
+    // pass 1: validate everything before any upload
     for (int i = 0; i < n_jobs; ++i) {
         const qsrt_decode_job& s = jobs[i];
-        const bool ok = s.words && s.row_scale && s.col_scale && s.out && s.rows >= 0 && s.cols >= 0 &&
-                        s.rows % 128 == 0 && s.cols % 128 == 0 && s.out_ld >= s.cols && s.out_ld % 8 == 0 &&
-                        reinterpret_cast<uintptr_t>(s.words) % 16 == 0 && s.tile_row_stride % 8 == 0 &&
-                        s.tile_col_stride % 8 == 0 && s.block_row_stride % 8 == 0 && s.block_col_stride % 8 == 0 &&
-                        reinterpret_cast<uintptr_t>(s.out) % 16 == 0 &&
-                        reinterpret_cast<uintptr_t>(s.col_scale) % 16 == 0 &&
-                        reinterpret_cast<uintptr_t>(s.row_scale) % 16 == 0;
-        if (!ok) {
-            free(host);
+        if (!job_ok(s))
             return qsrt::fail(qsrt::kBadArgument,
                               "decode job %d: need rows, cols multiples of 128, out_ld >= cols and a multiple of 8, "
                               "16-byte aligned words, out, row_scale and col_scale, tile and block strides multiples of 8, "
                               "non-null pointers",
                               i);
-        }
-        if (s.rows / 128 >= (1 << 30) || s.cols / 128 >= (1 << 30)) {
-            free(host);
+        if (s.rows / 128 >= (1 << 30) || s.cols / 128 >= (1 << 30))
             return qsrt::fail(qsrt::kBadArgument, "decode job %d is too large", i);
-        }
-        if (s.rows == 0 || s.cols == 0) continue;  // nothing to decode; the kernel never sees empty jobs
-        host[kept++] = Job{s.words,
-                           s.tile_row_stride,
-                           s.tile_col_stride,
-                           s.block_row_stride ? s.block_row_stride : 8 * s.tile_row_stride,
-                           s.block_col_stride ? s.block_col_stride : 8 * s.tile_col_stride,
-                           s.row_scale,
-                           s.col_scale,
-                           s.out,
-                           s.out_ld,
-                           static_cast<int32_t>(s.rows / 128),
-                           static_cast<int32_t>(s.cols / 128),
-                           total};
-        total += (s.rows / 128) * (s.cols / 128);
     }
-    // pageable source: the call returns once the table is staged, so the host copy can go
-    const hipError_t cp =
-        kept ? hipMemcpyAsync(workspace, host, sizeof(Job) * kept, hipMemcpyHostToDevice, stream) : hipSuccess;
-    free(host);
-    if (cp != hipSuccess) return qsrt::fail(qsrt::kHipError, "job upload failed: %s", hipGetErrorString(cp));
+    // pass 2: convert and upload in chunks (empty jobs are dropped: the kernel never sees them)
+    Job* table = static_cast<Job*>(workspace);
+    JobChunk chunk;
+    chunk.count = 0;
+    int64_t total = 0;
+    int kept = 0;
+    for (int i = 0; i < n_jobs; ++i) {
+        const qsrt_decode_job& s = jobs[i];
+        if (s.rows == 0 || s.cols == 0) continue;
+        chunk.jobs[chunk.count++] = Job{s.words,
+                                        s.tile_row_stride,
+                                        s.tile_col_stride,
+                                        s.block_row_stride ? s.block_row_stride : 8 * s.tile_row_stride,
+                                        s.block_col_stride ? s.block_col_stride : 8 * s.tile_col_stride,
+                                        s.row_scale,
+                                        s.col_scale,
+                                        s.out,
+                                        s.out_ld,
+                                        static_cast<int32_t>(s.rows / 128),
+                                        static_cast<int32_t>(s.cols / 128),
+                                        total};
+        total += (s.rows / 128) * (s.cols / 128);
+        if (chunk.count == kUploadChunk || i == n_jobs - 1) {
+            hipLaunchKernelGGL(upload_jobs_kernel, dim3(1), dim3(64), 0, stream, chunk, table + kept);
+            QSRT_HIP_TRY(hipGetLastError());
+            kept += chunk.count;
+            chunk.count = 0;
+        }
+    }
+    if (chunk.count) {  // the last job was empty: flush what is pending
+        hipLaunchKernelGGL(upload_jobs_kernel, dim3(1), dim3(64), 0, stream, chunk, table + kept);
+        QSRT_HIP_TRY(hipGetLastError());
+        kept += chunk.count;
+    }
     *plan = qsrt_decode_plan{workspace, kept, K, total};
     return qsrt::kOk;
 }
@@ -493,3 +520,4 @@ int qsrt_decode(const qsrt_decode_job* jobs, int n_jobs, int K, const uint8_t* l
 }
 
 }  // extern "C"
+
