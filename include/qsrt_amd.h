@@ -167,6 +167,22 @@ int qsrt_decode_execute(const qsrt_decode_plan *plan, const uint8_t *lut_e4m3, i
                         void *stream);
 
 /*
+ * qsrt_decode with no workspace argument and no allocation of any kind: the
+ * job table lives in the library's own device array (`scratch` in decode.hip,
+ * 4096 jobs = 352 KiB, held by each GPU the library runs on until the process
+ * ends) and is written by a stream-ordered upload kernel, so the call issues
+ * only kernel launches.  Same arguments, validation and results as
+ * qsrt_decode; n_jobs > 4096 is rejected (-1).  Every call on one GPU shares
+ * that GPU's table, so calls that overlap on one GPU (different streams or
+ * threads without ordering) race; calls ordered on one stream do not.
+ * No counterpart in the reference: it exists for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).
+ */
+int qsrt_decode_noalloc(const qsrt_decode_job *jobs, int n_jobs, int K, const uint8_t *lut_e4m3, int exact_fp8,
+                        int out_dtype, void *stream);
+
+/*
  * C[M, N] += alpha * A^T (B - B2) on the matrix cores, all row-major:
  *   A [K, M] (lda), B and B2 [K, N] (ldb), C [M, N] f32 (ldc).
  *   dtype 0: f32 operands (16-byte aligned, lda/ldb multiples of 4), exact

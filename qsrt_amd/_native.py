@@ -41,6 +41,7 @@ SIGNATURES: dict[str, tuple] = {
     "qsrt_decode": (_c_int, [_c_void_p, _c_int, _c_int, _c_void_p, _c_int, _c_int, _c_void_p, _c_size, _c_void_p]),
     "qsrt_decode_prepare": (_c_int, [_c_void_p, _c_int, _c_int, _c_void_p, _c_size, _c_void_p, _c_void_p]),
     "qsrt_decode_execute": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
+    "qsrt_decode_noalloc": (_c_int, [_c_void_p, _c_int, _c_int, _c_void_p, _c_int, _c_int, _c_void_p]),
     "qsrt_gemm_tn": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float,

@@ -45,6 +45,7 @@
 // (labels widened exactly to FP32), with the same data movement.
 
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
 #include "qsrt_amd.h"
@@ -411,6 +412,40 @@ bool job_ok(const qsrt_decode_job& s) {
            reinterpret_cast<uintptr_t>(s.row_scale) % 16 == 0;
 }
 
+// Most jobs the no-allocation decode holds (its job table is `scratch`).
+constexpr int kStaticJobs = 4096;
+
+}  // namespace
+
+// Device job table of qsrt_decode_noalloc: every GPU the library runs on holds
+// one copy (352 KiB) until the process ends.  Host code never uses this name
+// as an address; it uses the per-device address from hipGetSymbolAddress.
+static __device__ __align__(256) Job scratch[kStaticJobs];
+
+namespace {
+
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[64] = {nullptr};
+
+// Address of this device's `scratch`, looked up once per device with that
+// device current (each GPU holds its own copy at its own address).
+int scratch_table(Job** out) {
+    int dev = 0;
+    QSRT_HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return qsrt::fail(qsrt::kBadArgument, "device %d is out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return qsrt::fail(qsrt::kHipError, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                              hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = static_cast<Job*>(g_scratch_ptr[dev]);
+    return qsrt::kOk;
+}
+
 }  // namespace
 
 extern "C" {
@@ -521,3 +556,16 @@ int qsrt_decode(const qsrt_decode_job* jobs, int n_jobs, int K, const uint8_t* l
 
 }  // extern "C"
 
+extern "C" int qsrt_decode_noalloc(const qsrt_decode_job* jobs, int n_jobs, int K, const uint8_t* lut_e4m3,
+                                   int exact_fp8, int out_dtype, void* stream) {
+    if (out_dtype != 0 && out_dtype != 1) return qsrt::fail(qsrt::kBadArgument, "out_dtype must be 0 (bf16) or 1 (f32)");
+    if (n_jobs > kStaticJobs)
+        return qsrt::fail(qsrt::kBadArgument, "qsrt_decode_noalloc holds at most %d jobs; got %d (use qsrt_decode "
+                          "with a workspace)", kStaticJobs, n_jobs);
+    if (n_jobs > 0 && !lut_e4m3) return qsrt::fail(qsrt::kBadArgument, "null pointer argument");
+    Job* table = nullptr;
+    if (const int rc = scratch_table(&table)) return rc;
+    qsrt_decode_plan plan;
+    if (const int rc = qsrt_decode_prepare(jobs, n_jobs, K, table, sizeof(Job) * kStaticJobs, &plan, stream)) return rc;
+    return qsrt_decode_execute(&plan, lut_e4m3, exact_fp8, out_dtype, stream);
+}
