@@ -10,6 +10,9 @@ Restates, from the reference:
 * the tensor-core permutation (``qsrt/exl3_reference.py:86-105``) -- pinned
   as a bijection against the closed form below (rows 2(t%4)+{0,1,8,9},
   columns t//4 + {0,8});
+* the record-major container (``qsrt/qsrt.py:1051-1172``): 128-channel
+  records along the rate axis, each the EXL words of its tiles in row-major
+  tile order -- pinned by round trips against ``pack_words`` on every record;
 * the normalised Sylvester Hadamard and the decode chain
   (``qsrt/exl3_reference.py:108-140``, ``:210-243``, ``:280-302``) -- pinned
   by H H^T = I, symmetry, and the H_2 Kronecker closed form.
@@ -48,6 +51,34 @@ def unpack_symbols(words: np.ndarray, bits: int) -> np.ndarray:
     for b in range(bits):
         sym |= stream[..., b::bits] << (bits - 1 - b)
     return sym
+
+
+def unpack_records(payload: np.ndarray, record_bits, rate_axis: str, k_tiles: int, n_tiles: int):
+    """Record-major payload -> ``(states uint16 [k_tiles, n_tiles, 256],
+    tile_bits [k_tiles, n_tiles])``.  Record ``r`` holds the 8 rate-axis tiles
+    ``8r .. 8r + 7`` across the whole other axis, tiles in row-major order of
+    that ``[rows, cols]`` strip, each ``16 K`` words at the record's rate."""
+
+    words = np.asarray(payload).reshape(-1).view(np.uint16) if np.asarray(payload).dtype == np.int16 else \
+        np.asarray(payload, dtype=np.uint16).reshape(-1)
+    states = np.zeros((k_tiles, n_tiles, TILE), dtype=np.uint16)
+    tile_bits = np.zeros((k_tiles, n_tiles), dtype=np.int64)
+    cursor = 0
+    for r, bits in enumerate(record_bits):
+        if rate_axis == "k":
+            rows, cols = slice(8 * r, 8 * r + 8), slice(0, n_tiles)
+            shape = (8, n_tiles)
+        else:
+            rows, cols = slice(0, k_tiles), slice(8 * r, 8 * r + 8)
+            shape = (k_tiles, 8)
+        count = shape[0] * shape[1] * 16 * bits
+        chunk = words[cursor:cursor + count].reshape(shape[0], shape[1], 16 * bits)
+        states[rows, cols] = cyclic_states(unpack_symbols(chunk, bits), bits)
+        tile_bits[rows, cols] = bits
+        cursor += count
+    if cursor != words.size:
+        raise ValueError("payload length does not match its records")
+    return states, tile_bits
 
 
 def cyclic_states(edges: np.ndarray, bits: int) -> np.ndarray:

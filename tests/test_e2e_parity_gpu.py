@@ -30,6 +30,7 @@ import torch
 import bench
 from oracle import encode as oenc
 from oracle import fmt as ofmt
+from oracle import ldlq as oldlq
 from oracle import tables as otables
 from qsrt_amd import exl3_encoder_backend as be
 from qsrt_amd.ldlq import make_shared_h
@@ -136,3 +137,65 @@ def test_config3_strip_matches_cpu_encode():
     W = bench.student_t_like((n, k), std=0.015, gen=gen).bfloat16().float().T.contiguous()
     xd = x.double()
     _check_matrix("config 3 strip", W, (xd.T @ xd).float(), rows, 3, default_qsrt_transform_seeds(1, "w1"))
+
+
+def test_few_row_hessian_matches_cpu_encode():
+    """A Hessian from 48 calibration rows (rank 48 of 256 plus 1% damping, the
+    conditioning of a rarely routed expert): the device factorisation must
+    still agree with the float64 one closely enough that the payloads match."""
+
+    d = bench.config_expert(1, torch.device("cpu"), tokens=48)
+    x = d["x"].double()
+    _check_matrix("config 1 w1, 48 rows", d["w_gate"].T.contiguous(), (x.T @ x).float(), 48, 2,
+                  default_qsrt_transform_seeds(1, "w1"))
+
+
+def test_batch_conditioned_path_matches_cpu_encode():
+    """``quantize_qsrt_batch`` (the layer pipeline's path): w1 and w3 of one
+    expert share a 96-row Hessian; the congruence uses the regularised su,
+    the input profile is layer-shared (taken from w1), the global scale goes
+    into sv, and the records along N mix K3 and K4."""
+
+    k, n, rows = 512, 256, 96
+    gen = torch.Generator().manual_seed(20261201 + 51)
+    x = bench.ar1_scan(rows, k, 0.85, gen).double()
+    H_sum = (x.T @ x).float()
+    Ws = [bench.student_t_like((n, k), std=0.015, gen=gen).bfloat16().float().T.contiguous() for _ in range(2)]
+    bits_map = (3,) * 8 + (4,) * 8
+    scope = ("e2e-batch-test", 1)
+    hds, groups = [], []
+    for matrix in ("w1", "w3"):
+        seeds = default_qsrt_transform_seeds(1, matrix)
+        hd = make_shared_h(k, DEV, H_sum)
+        hd["count"] = rows
+        hds.append(hd)
+        groups.append([{"K": 3, "seed": seeds.input_sign, "sv_seed": seeds.output_sign, "sigma_reg": 0.01,
+                        "devices": [str(DEV)], "apply_out_scales": False, "tailbite_context": 128,
+                        "sqg_e4m3_luts_by_bits": {b: sqg_xor_cheb_t12_bytes(b) for b in (2, 3, 4)},
+                        "mixed_rate_axis": "n", "mixed_tile_bits": bits_map,
+                        "shared_input_scales_key": (scope, "w1"), "g_scale_into_sv": True}])
+    _say(f"[e2e] quantize_qsrt_batch: w1, w3 [{k} x {n}], {rows}-row Hessian, records K3/K4 along N")
+    out = be.quantize_qsrt_batch([W.to(DEV).clone() for W in Ws], hds, groups)
+    torch.cuda.synchronize()
+    be._SHARED_INPUT_SCALES.pop((scope, "w1"), None)
+    labels = {b: otables.t12_values(b) for b in (3, 4)}
+    lags = {3: 1, 4: 1}
+    tile_bits = np.tile(np.array(bits_map), (k // 16, 1))
+    profile = None
+    for (matrix, W, res, qa) in zip(("w1", "w3"), Ws, out, groups):
+        seeds = default_qsrt_transform_seeds(1, matrix)
+        su_s, sv_s = _signs(k, seeds.input_sign), _signs(n, seeds.output_sign)
+        Wd = W.double().numpy()
+        if profile is None:
+            profile = oldlq.input_rms(Wd, sv_s)
+        cpu = oenc.encode_matrix(Wd, H_sum.double().numpy(), rows, su_s, sv_s, res[0]["g_scale"], tile_bits, labels,
+                                 lags, sigma_reg=0.01, conditioned=True, g_into_sv=True, input_scales=profile)
+        g_states = res[0]["encoded"].cpu().numpy().view(np.uint16)
+        stats = oenc.compare_states(g_states, cpu, labels, tile_bits)
+        deltas = stats["sse_rel_deltas"]
+        _say(f"[e2e] batch {matrix}: {stats['differ']} of {stats['tiles']} tiles differ, max near-tie SSE delta "
+             f"{max(deltas) if deltas else 0.0:.3e}; proxy GPU {res[0]['proxy']:.6f} CPU "
+             f"{oenc.proxy(cpu['W_r'], cpu['Q'], cpu['H_c']):.6f}")
+        for dlt in deltas:
+            assert dlt <= TIE_SSE_REL
+        assert stats["mismatch_rate"] <= 0.01
