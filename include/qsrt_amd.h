@@ -58,6 +58,20 @@ int qsrt_viterbi_tiles(const float *tiles, float *recon, uint16_t *states, int64
                        size_t workspace_bytes, void *stream);
 
 /*
+ * qsrt_viterbi_tiles on at most `max_workgroups` compute units (0: all of
+ * them).  Two rate groups of one BlockLDLQ step launched on two streams
+ * with grids in proportion to their work run side by side instead of one
+ * after the other (each workgroup holds a whole CU).  The workspace needs
+ * at most qsrt_viterbi_workspace_bytes(K, n_tiles) bytes.  Same results as
+ * qsrt_viterbi_tiles for any grid.  No counterpart in the reference, whose
+ * launcher always sizes the grid from the tile count
+ * (qsrt/csrc/sqg_quantize.cu:507-576).
+ */
+int qsrt_viterbi_tiles_ex(const float *tiles, float *recon, uint16_t *states, int64_t n_tiles, int K,
+                          int tailbite_context, const uint8_t *lut_e4m3, int boundary_lag, int max_workgroups,
+                          void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * EXL word packing of n_tiles tiles at rate K (1..6; the QSRT container uses
  * 2..4, the uniform codec paths of qsrt/qsrt_codec_pilot.py:220-281 up to 6):
  *   states u16 [n_tiles, 256] (only the low K bits are stored; 16-byte

@@ -659,7 +659,15 @@ size_t qsrt_viterbi_workspace_bytes(int K, int64_t n_tiles) {
 int qsrt_viterbi_tiles(const float* tiles, float* recon, uint16_t* states, int64_t n_tiles, int K,
                        int tailbite_context, const uint8_t* lut_e4m3, int boundary_lag, void* workspace,
                        size_t workspace_bytes, void* stream_handle) {
+    return qsrt_viterbi_tiles_ex(tiles, recon, states, n_tiles, K, tailbite_context, lut_e4m3, boundary_lag, 0,
+                                 workspace, workspace_bytes, stream_handle);
+}
+
+int qsrt_viterbi_tiles_ex(const float* tiles, float* recon, uint16_t* states, int64_t n_tiles, int K,
+                          int tailbite_context, const uint8_t* lut_e4m3, int boundary_lag, int max_workgroups,
+                          void* workspace, size_t workspace_bytes, void* stream_handle) {
     hipStream_t stream = static_cast<hipStream_t>(stream_handle);
+    if (max_workgroups < 0) return qsrt::fail(qsrt::kBadArgument, "max_workgroups must be non-negative");
     if (K < 1 || K > 6)
         return qsrt::fail(qsrt::kBadArgument, "K%d is not supported by the MI355X tile kernel (K1..K6)", K);
     if (tailbite_context < 1 || tailbite_context > 128)
@@ -672,7 +680,7 @@ int qsrt_viterbi_tiles(const float* tiles, float* recon, uint16_t* states, int64
         return qsrt::fail(qsrt::kBadArgument, "null pointer argument");
     int cus = 0;
     if (int rc = qsrt::current_cu_count(&cus)) return rc;
-    const int grid = launch_workgroups(n_tiles, cus);
+    const int grid = launch_workgroups(n_tiles, max_workgroups > 0 && max_workgroups < cus ? max_workgroups : cus);
     const size_t need = workgroup_dec_bytes(K) * static_cast<size_t>(grid);
     if (workspace_bytes < need)
         return qsrt::fail(qsrt::kWorkspaceTooSmall, "workspace too small: %zu < %zu bytes", workspace_bytes, need);

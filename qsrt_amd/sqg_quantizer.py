@@ -36,22 +36,28 @@ from .sqg_e4m3 import sqg_e4m3_bytes
 # kernel (qsrt_quantize_tiles_k2_kernel.cuh:45).
 K2_FAST_MAX_LABEL = 16.0
 
-_workspaces: dict[int, torch.Tensor] = {}
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def _workspace(device: torch.device, bits: int, n_tiles: int) -> torch.Tensor:
+    """Traceback workspace of the current stream on ``device``.  Each stream
+    has its own buffer (sized once for the widest grid), so launches queued
+    on different streams never share decision rows; launches on one stream
+    are ordered and reuse it."""
+
     need = int(_native.lib().qsrt_viterbi_workspace_bytes(bits, n_tiles))
     if need == 0:
         raise _native.NativeError(
             "qsrt_viterbi_workspace_bytes failed: " + _native.lib().qsrt_last_error().decode()
         )
     index = device.index if device.index is not None else torch.cuda.current_device()
-    ws = _workspaces.get(index)
+    key = (index, torch.cuda.current_stream(device).cuda_stream)
+    ws = _workspaces.get(key)
     if ws is None or ws.numel() < need:
-        # Size for the widest grid (one workgroup per CU, 1 MiB each) once.
-        full = int(_native.lib().qsrt_viterbi_workspace_bytes(2, 1 << 30))
+        # Size for the widest grid (one workgroup per CU) once.
+        full = max(int(_native.lib().qsrt_viterbi_workspace_bytes(b, 1 << 30)) for b in range(1, 7))
         ws = torch.empty(max(need, full), dtype=torch.uint8, device=device)
-        _workspaces[index] = ws
+        _workspaces[key] = ws
     return ws
 
 
@@ -106,9 +112,11 @@ def viterbi_tiles(
     tailbite_context: int = 128,
     lag: int = 0,
     out: tuple[torch.Tensor, torch.Tensor] | None = None,
+    max_workgroups: int = 0,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Run the HIP tile Viterbi.  ``tiles`` FP32 ``[T, 256]`` (tensor-core
     order), ``lut`` the state-indexed uint8 E4M3 table on the same device.
+    ``max_workgroups`` caps the grid (0: one workgroup per CU).
     Returns ``(recon f32 [T, 256], states int16 [T, 256])``."""
 
     if not tiles.is_cuda:
@@ -131,11 +139,12 @@ def viterbi_tiles(
         return recon, states
     ws = _workspace(tiles.device, bits, n)
     with torch.cuda.device(tiles.device):
-        rc = _native.lib().qsrt_viterbi_tiles(
+        rc = _native.lib().qsrt_viterbi_tiles_ex(
             tiles.data_ptr(), recon.data_ptr(), states.data_ptr(), n, int(bits), int(tailbite_context),
-            lut.data_ptr(), int(lag), ws.data_ptr(), ws.numel(), _native.stream_handle(tiles.device),
+            lut.data_ptr(), int(lag), int(max_workgroups), ws.data_ptr(), ws.numel(),
+            _native.stream_handle(tiles.device),
         )
-    _native.check(rc, "qsrt_viterbi_tiles")
+    _native.check(rc, "qsrt_viterbi_tiles_ex")
     return recon, states
 
 
@@ -218,7 +227,8 @@ def quantize_tiles_sqg(tiles: torch.Tensor, quant_args: dict) -> tuple[torch.Ten
     context = int(quant_args.get("tailbite_context", 128))
     if not 1 <= context <= 128:
         raise ValueError("tailbite_context must be in 1..128")
-    output, indices = viterbi_tiles(tiles, lut, bits, tailbite_context=context, lag=lag)
+    output, indices = viterbi_tiles(tiles, lut, bits, tailbite_context=context, lag=lag,
+                                    max_workgroups=int(quant_args.get("tile_workgroups", 0)))
     if os.environ.get("QSRT_DEBUG_TILE_CLOSURE") == "1":
         debug_check_trellis_closure(indices, bits)
     return output, indices
