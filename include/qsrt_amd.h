@@ -209,6 +209,38 @@ int qsrt_decode_noalloc(const qsrt_decode_job *jobs, int n_jobs, int K, const ui
 int qsrt_gemm_tn(float *C, const void *A, const void *B, const void *B2, int64_t M, int64_t N, int64_t K,
                  int64_t lda, int64_t ldb, int64_t ldc, float alpha, int dtype, void *stream);
 
+/*
+ * BlockLDLQ step, batched over B members (member m quantizes source
+ * src[m]).  For the 16-row block [blk, blk + 16) of a span ending at row
+ * `end`, every member's target
+ *   T_m = W_s[blk] + mult[m] * (P_m[blk] + L_s[blk+16:end, blk:blk+16]^T (W_s - Q_m)[blk+16:end])
+ * is written, one 16 x 16 tile per 16 columns in tensor-core order, to tile
+ * slot[m * N/16 + t] of `tiles` ([slots, 256] f32; the caller groups slots
+ * by rate).  W [S, K, N], L [S, K, K], Q and P [B, K, N]: row-major f32 with
+ * batch strides sW, sL, sQ, sP (elements); src int32 [B] device, mult f32 [B]
+ * device, slot int32 [B * N/16] device.  K and N multiples of 16, blk a
+ * multiple of 16 with blk + 16 <= end <= K.  Each element sums P first, then
+ * the products in increasing row order, independent of B and N.
+ * Replaces the per-step clone, product (prod_cache + L^T (W - Q)), add,
+ * stack and tensor-core gather of ldlq / ldlq_mixed_batched
+ * (qsrt/exl3_encoder_backend.py:420-539, :1190-1478).
+ */
+int qsrt_ldlq_targets(float *tiles, const float *W, const float *L, const float *Q, const float *P,
+                      const int32_t *src, const float *mult, const int32_t *slot, int B, int64_t K, int64_t N,
+                      int64_t sW, int64_t sL, int64_t sQ, int64_t sP, int64_t blk, int64_t end, void *stream);
+
+/*
+ * Commit of a BlockLDLQ step: rows [blk, blk + 16) of every Q_m ([B, K, N]
+ * f32, batch stride sQ) take the reconstruction tiles recon[slot[m N/16 + t]]
+ * (tensor-core order, f32 [slots, 256]) and tile row blk / 16 of every
+ * encoded_m ([B, K/16, N/16, 256] int16, batch stride sE) the states
+ * states[slot[...]] (u16 [slots, 256]).  Replaces the scatter of the
+ * reconstruction and states after each tile call (reference :1055-1070,
+ * :1419-1440).
+ */
+int qsrt_ldlq_commit(float *Q, int16_t *encoded, const float *recon, const uint16_t *states, const int32_t *slot,
+                     int B, int64_t K, int64_t N, int64_t sQ, int64_t sE, int64_t blk, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

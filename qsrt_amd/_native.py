@@ -52,6 +52,16 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float,
          _c_int, _c_void_p],
     ),
+    "qsrt_ldlq_targets": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p],
+    ),
+    "qsrt_ldlq_commit": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_void_p],
+    ),
     "qsrt_hadamard": (
         _c_int,
         [_c_void_p, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
