@@ -25,8 +25,9 @@ warm-up expert W times first.  Prints ONE JSON line:
                matrix, with the same inputs the GPU encoded
   parity       the GPU's states on that sample against the CPU oracle's
 Secondary keys: the decode of the encoded layer, the config-2 Viterbi
-microbench (packing inside its step), the config-4 expert at K3, the MFMA
-GEMMs and the Hadamard rotation.
+microbench (packing inside its step), the config-4 expert at K3 (the
+north-star target) and at K2 (as BASELINE specifies it), the config-3 GLM
+expert, the MFMA GEMMs and the Hadamard rotation.
 """
 
 from __future__ import annotations
@@ -674,6 +675,88 @@ def expert_bench(bits: int = 3, reps: int = 2) -> dict:
             "proxy_err": {m: round(res[m]["proxy"], 5) for m in ("w1", "w3", "w2")}}
 
 
+def glm_expert_bench(reps: int = 2) -> dict:
+    """the GLM-class SwiGLU expert (hidden 5120, inter
+    1536) at K3 with 8 outlier channels, 128-block Hadamard rotation, H13
+    from 8192 AR(1) rows (rho 0.9) and H2 from the source SwiGLU
+    activations, all three matrices through ``quantize_qsrt_batch``."""
+
+    from qsrt_amd import exl3_encoder_backend as be
+    from qsrt_amd import gemm
+    from qsrt_amd.ldlq import make_shared_h
+    from qsrt_amd.sqg_e4m3 import sqg_xor_cheb_t12_bytes
+    from qsrt_amd.transform_seeds import default_qsrt_transform_seeds
+
+    dev = torch.device("cuda:0")
+    d = config_expert(3, dev)
+    hidden, inter, x = d["hidden"], d["inter"], d["x"]
+    luts = {b: sqg_xor_cheb_t12_bytes(b) for b in (2, 3, 4)}
+
+    def qa(matrix, k, n):
+        seeds = default_qsrt_transform_seeds(1, matrix)
+        axis = "k" if matrix == "w2" else "n"
+        return {"K": 3, "seed": seeds.input_sign, "sv_seed": seeds.output_sign, "sigma_reg": 0.01,
+                "devices": [str(dev)], "apply_out_scales": False, "tailbite_context": CONTEXT,
+                "sqg_e4m3_luts_by_bits": luts, "mixed_rate_axis": axis,
+                "mixed_tile_bits": (3,) * ((k if axis == "k" else n) // 16)}
+
+    times, proxies = [], {}
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        h13 = gemm.gram_(torch.zeros((hidden, hidden), device=dev), x)
+        h = (torch.nn.functional.silu(x @ d["w_gate"].T) * (x @ d["w_up"].T)).contiguous()
+        h2 = gemm.gram_(torch.zeros((inter, inter), device=dev), h)
+        del h
+        ws, hs, qas = [], [], []
+        for matrix, w, H in (("w1", d["w_gate"], h13), ("w3", d["w_up"], h13)):
+            shared = make_shared_h(hidden, dev, H)
+            shared["count"] = x.shape[0]
+            ws.append(w.T.contiguous())
+            hs.append(shared)
+            qas.append([qa(matrix, hidden, inter)])
+        up = be.quantize_qsrt_batch(ws, hs, qas, return_weight_q=False)
+        shared = make_shared_h(inter, dev, h2)
+        shared["count"] = x.shape[0]
+        down = be.quantize_qsrt_batch([d["w_down"].T.contiguous()], [shared], [[qa("w2", inter, hidden)]],
+                                      return_weight_q=False)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+        proxies = {"w1": up[0][0]["proxy"], "w3": up[1][0]["proxy"], "w2": down[0][0]["proxy"]}
+    weights = 3 * hidden * inter
+    return {"workload": "config 3: GLM-class SwiGLU expert, gate/up [5120 x 1536] and down [1536 x 5120], K3, "
+                        "8 outlier channels (20x variance), H13 from 8192 AR(1) rows (rho 0.9), H2 from the source "
+                        "SwiGLU activations, 128-block Hadamard, BlockLDLQ",
+            "seconds": round(times[-1], 3), "seconds_first": round(times[0], 3),
+            "M_weights_per_s": round(weights / times[-1] / 1e6, 2),
+            "proxy_err": {m: round(v, 5) for m, v in proxies.items()}}
+
+
+def k2_expert_bench(reps: int = 2) -> dict:
+    """BASELINE config 4 as specified: the coupled Kimi-class expert at K2
+    (one fp16 suh and svh vector per matrix, about 2.01 bpw all told)."""
+
+    dev = torch.device("cuda:0")
+    src = expert_source(4, dev)
+    enc = ExpertEncoder(dev, hidden=LAYER_HIDDEN, inter=LAYER_INTER, record_bits=(2,) * (LAYER_INTER // 128),
+                        scope=("bench-expert", 2))
+    times = []
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        res = enc.encode([src])[0]
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    weights = 3 * LAYER_HIDDEN * LAYER_INTER
+    bits = sum(res[m]["words"].numel() * 16 + 16 * (res[m]["suh"].numel() + res[m]["svh"].numel())
+               for m in ("w1", "w3", "w2"))
+    return {"workload": "config 4: coupled Kimi-class expert 7168 x 2048 SwiGLU at K2, all three matrices, LDLQ, "
+                        "H2 from reconstructed activations, fp16 suh/svh vectors",
+            "seconds": round(times[-1], 3), "seconds_first": round(times[0], 3),
+            "M_weights_per_s": round(weights / times[-1] / 1e6, 2), "bpw": round(bits / weights, 5),
+            "proxy_err": {m: round(res[m]["proxy"], 5) for m in ("w1", "w3", "w2")}}
+
+
 def gemm_bench(steps: int = 5):
     """The two MFMA GEMM shapes of the config-4 expert encode:
     Hessian capture ``H += X^T X`` of 16,384 bf16 tokens x 7168 channels,
@@ -852,6 +935,9 @@ def main() -> int:
         if "cpu_baseline" in result:
             result["expert_encode"]["speedup_vs_cpu_baseline"] = round(
                 result["expert_encode"]["M_weights_per_s"] / result["cpu_baseline"]["value"], 1)
+        log("[bench] config-3 GLM expert (K3) and config-4 expert at K2")
+        result["glm_expert_encode"] = glm_expert_bench()
+        result["expert_encode_k2"] = k2_expert_bench()
         log("[bench] GEMM and Hadamard kernels")
         result["gemm"] = gemm_bench()
         result["hadamard"] = hadamard_bench()
