@@ -361,20 +361,22 @@ def layer_sources(device, experts, counts) -> list[dict]:
     return [expert_source(5, device, expert=e, tokens=counts[e]) for e in experts]
 
 
-def layer_bench(steps: int, warmup: int):
+def layer_bench(steps: int, warmup: int, experts: int = LAYER_EXPERTS):
     """The headline: the whole config-5 layer, encoded in ``steps`` timed
     steps of consecutive experts after ``warmup`` encodes of a warm-up
-    expert, then decoded to bf16."""
+    expert, then decoded to bf16.  ``experts`` < 384 encodes only the first
+    experts of the same routed layer (shorter profiling passes)."""
 
     from qsrt_amd import exl3_encoder_backend as be
 
     dev = torch.device("cuda:0")
     counts = zipf_token_counts()
-    steps = max(1, min(steps, LAYER_EXPERTS))
-    bounds = [LAYER_EXPERTS * i // steps for i in range(steps + 1)]
-    log(f"[bench] layer inputs: {LAYER_EXPERTS} experts x bf16 gate/up/down + {sum(counts)} routed rows, to HBM")
+    experts = max(1, min(experts, LAYER_EXPERTS))
+    steps = max(1, min(steps, experts))
+    bounds = [experts * i // steps for i in range(steps + 1)]
+    log(f"[bench] layer inputs: {experts} experts x bf16 gate/up/down + {sum(counts[:experts])} routed rows, to HBM")
     t0 = time.perf_counter()
-    sources = layer_sources(dev, range(LAYER_EXPERTS), counts)
+    sources = layer_sources(dev, range(experts), counts)
     warm = expert_source(5, dev, expert=LAYER_EXPERTS, tokens=max(counts))
     torch.cuda.synchronize()
     log(f"[bench] layer inputs ready in {time.perf_counter() - t0:.1f} s")
@@ -409,10 +411,10 @@ def layer_bench(steps: int, warmup: int):
         wall = time.perf_counter() - t_start
         timer.active = False
         vit = timer.summary()
-    weights = LAYER_EXPERTS * 3 * LAYER_HIDDEN * LAYER_INTER
+    weights = experts * 3 * LAYER_HIDDEN * LAYER_INTER
     proxies = [e[m]["proxy"] for e in encoded for m in ("w1", "w3", "w2")]
     del sources
-    return {"wall": wall, "steps": steps, "step_s": step_s, "weights": weights, "viterbi": vit, "encoded": encoded,
+    return {"wall": wall, "steps": steps, "experts": experts, "step_s": step_s, "weights": weights, "viterbi": vit, "encoded": encoded,
             "proxy_mean": sum(proxies) / len(proxies), "proxy_max": max(proxies), "warm": warm, "counts": counts}
 
 
@@ -836,26 +838,10 @@ def copy_calibration(nbytes: int) -> None:
     log(f"[bench] copied {nbytes} bytes")
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20, help="timed steps the 384-expert layer is split into")
-    ap.add_argument("--warmup", type=int, default=2, help="untimed encodes of a warm-up expert")
-    ap.add_argument("--no-secondary", action="store_true", help="only the layer encode, its decode and its CPU sample")
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
-                    help="only run a device copy of BYTES (reference for HBM byte counters)")
-    args = ap.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one MI355X: this build runs the encoder on one GPU and does not shard it "
-              "across GPUs (experts would shard with no exchange; see the repository's design notes)",
-              file=sys.stderr)
-        return 2
-    if args.copy_calibration:
-        copy_calibration(args.copy_calibration)
-        return 0
+LINES = ("layer", "microbench", "expert", "glm", "k2", "gemm", "hadamard")
 
-    lay = layer_bench(args.steps, args.warmup)
+
+def headline(lay: dict, warmup: int) -> dict:
     vit = lay["viterbi"]
     # a launch on a split grid holds only its share of the GPU: its duration counts at that share
     mean_launch_ms = vit["gpu_ms"] / max(vit["launches"], 1)
@@ -863,13 +849,19 @@ def main() -> int:
     flops_per_launch = mean_tiles * 256 * EDGES_PER_WEIGHT * FLOPS_PER_EDGE
     achieved = flops_per_launch / (mean_launch_ms / 1e3) / 1e12
     value = lay["weights"] / lay["wall"] / 1e6
-    result = {
+    experts = lay["experts"]
+    for d in vit["by_rate"].values():
+        d["mean_ms"] = round(d["ms"] / max(d["launches"], 1), 4)
+        d["tiles_per_launch"] = round(d["tiles"] / max(d["launches"], 1), 1)
+    log(f"[bench] layer: {lay['wall']:.1f} s, {value:.2f} M weights/s; Viterbi {achieved:.1f} TFLOP/s, "
+        f"{100 * vit['gpu_ms'] / 1e3 / lay['wall']:.1f}% of wall")
+    return {
         "metric": "encoded weights/sec (M/s) at K=2/3 on one GPU",
         "value": round(value, 3),
         "unit": "M weights/s",
         "n_gpus": 1,
         "steps": lay["steps"],
-        "warmup": args.warmup,
+        "warmup": warmup,
         "ms_per_step": round(lay["wall"] / lay["steps"] * 1e3, 1),
         "higher_is_better": True,
         "scaling": "weak",
@@ -880,9 +872,10 @@ def main() -> int:
             "workload": "config 5 (BASELINE configs[4]): full Kimi-class MoE layer encode, 384 experts x "
                         "(gate, up [7168 x 2048], down [2048 x 7168]), exact coupled basis, Zipf s=1.1 routing of "
                         "65,536 calibration tokens, records 14 K3 + 2 K4 per matrix, BlockLDLQ, H2 from the "
-                        "reconstructed SwiGLU activations, L=16, C=128, sqg_xor_cheb_t12",
-            "experts": LAYER_EXPERTS, "weights": lay["weights"], "layer_seconds": round(lay["wall"], 2),
-            "experts_per_step": sorted({LAYER_EXPERTS * (i + 1) // lay["steps"] - LAYER_EXPERTS * i // lay["steps"]
+                        "reconstructed SwiGLU activations, L=16, C=128, sqg_xor_cheb_t12"
+                        + ("" if experts == LAYER_EXPERTS else f" -- PARTIAL: only the first {experts} experts"),
+            "experts": experts, "weights": lay["weights"], "layer_seconds": round(lay["wall"], 2),
+            "experts_per_step": sorted({experts * (i + 1) // lay["steps"] - experts * i // lay["steps"]
                                         for i in range(lay["steps"])}),
         },
         "roofline": {
@@ -898,7 +891,7 @@ def main() -> int:
             "mean_launch_ms": round(mean_launch_ms, 4),
             "mean_launch_ms_note": "HIP events around every launch on its stream, each duration weighted by the share "
                                    "of the CUs its grid holds (the K3 and K4 groups of a step run side by side on "
-                                   "split grids)",
+                                   "split grids); per rate, mean_ms is the unweighted event mean",
             "launches": vit["by_rate"],
             "viterbi_share_of_wall": round(vit["gpu_ms"] / 1e3 / lay["wall"], 4),
             # The 157.3 TFLOP/s peak counts packed FP32; this build disables packed FP32 ops (a miscompare hazard
@@ -908,38 +901,85 @@ def main() -> int:
         },
         "quality": {"proxy_err_mean": round(lay["proxy_mean"], 6), "proxy_err_max": round(lay["proxy_max"], 6)},
     }
-    log(f"[bench] layer: {lay['wall']:.1f} s, {value:.2f} M weights/s; Viterbi {achieved:.1f} TFLOP/s, "
-        f"{100 * vit['gpu_ms'] / 1e3 / lay['wall']:.1f}% of wall")
-    log("[bench] decode of the encoded layer")
-    result["decode"] = layer_decode(lay["encoded"])
-    log(f"[bench] decode {result['decode']['ms']} ms, {result['decode']['roofline']['achieved']} GB/s")
-    first = next(e for e in lay["encoded"] if "encoded" in e["w1"])
-    sample_src = expert_source(5, torch.device("cuda:0"), expert=first["expert"], tokens=first["tokens"])
-    del lay["encoded"]
-    torch.cuda.empty_cache()
-    if not args.no_cpu_baseline:
-        log("[bench] CPU baseline and parity on a sample of the layer")
-        cs = layer_cpu_sample(first, sample_src)
-        result["cpu_baseline"] = cs["cpu"]
-        result["cpu_baseline"]["gpu_speedup"] = round(value / cs["cpu"]["value"], 1)
-        result["parity"] = cs["parity"]
-        log(f"[bench] CPU {cs['cpu']['value']} M w/s on {cs['cpu']['cores']} threads; parity {json.dumps(cs['parity'])}")
-    del first, sample_src
-    if not args.no_secondary:
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20, help="timed steps the 384-expert layer is split into")
+    ap.add_argument("--warmup", type=int, default=2, help="untimed encodes of a warm-up expert")
+    ap.add_argument("--no-secondary", action="store_true", help="only the layer encode, its decode and its CPU sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", default=",".join(LINES),
+                    help=f"comma list of lines to run, from {','.join(LINES)} (profiling passes)")
+    ap.add_argument("--experts", type=int, default=LAYER_EXPERTS,
+                    help="encode only the first experts of the layer (profiling passes; the headline needs 384)")
+    ap.add_argument("--tiles", type=int, default=65536, help="tiles per rate of the config-2 microbench")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run a device copy of BYTES (reference for HBM byte counters)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: this build runs the encoder on one GPU and does not shard it "
+              "across GPUs (experts would shard with no exchange; see the repository's design notes)",
+              file=sys.stderr)
+        return 2
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return 0
+    lines = [x for x in args.only.split(",") if x]
+    bad = [x for x in lines if x not in LINES]
+    if bad:
+        print(f"bench.py: unknown --only lines {bad}; choose from {LINES}", file=sys.stderr)
+        return 2
+    if args.no_secondary:
+        lines = ["layer"]
+
+    result: dict = {}
+    if "layer" in lines:
+        lay = layer_bench(args.steps, args.warmup, args.experts)
+        result = headline(lay, args.warmup)
+        value = result["value"]
+        log("[bench] decode of the encoded layer")
+        result["decode"] = layer_decode(lay["encoded"])
+        log(f"[bench] decode {result['decode']['ms']} ms, {result['decode']['roofline']['achieved']} GB/s")
+        first = next(e for e in lay["encoded"] if "encoded" in e["w1"])
+        sample_src = expert_source(5, torch.device("cuda:0"), expert=first["expert"], tokens=first["tokens"])
+        del lay["encoded"]
+        torch.cuda.empty_cache()
+        if not args.no_cpu_baseline:
+            log("[bench] CPU baseline and parity on a sample of the layer")
+            cs = layer_cpu_sample(first, sample_src)
+            result["cpu_baseline"] = cs["cpu"]
+            result["cpu_baseline"]["gpu_speedup"] = round(value / cs["cpu"]["value"], 1)
+            result["parity"] = cs["parity"]
+            log(f"[bench] CPU {cs['cpu']['value']} M w/s on {cs['cpu']['cores']} threads; "
+                f"parity {json.dumps(cs['parity'])}")
+        del first, sample_src
+    else:
+        result = {"metric": "encoded weights/sec (M/s) at K=2/3 on one GPU", "value": None,
+                  "note": f"headline not run (--only {args.only})"}
+    if "microbench" in lines:
         log("[bench] config-2 microbench")
-        result["microbench"] = microbench()
+        result["microbench"] = microbench(args.tiles)
         if not args.no_cpu_baseline:
             result["microbench"]["cpu"] = microbench_cpu()
+    if "expert" in lines:
         log("[bench] config-4 expert (K3)")
         result["expert_encode"] = expert_bench()
         if "cpu_baseline" in result:
             result["expert_encode"]["speedup_vs_cpu_baseline"] = round(
                 result["expert_encode"]["M_weights_per_s"] / result["cpu_baseline"]["value"], 1)
-        log("[bench] config-3 GLM expert (K3) and config-4 expert at K2")
+    if "glm" in lines:
+        log("[bench] config-3 GLM expert (K3)")
         result["glm_expert_encode"] = glm_expert_bench()
+    if "k2" in lines:
+        log("[bench] config-4 expert at K2")
         result["expert_encode_k2"] = k2_expert_bench()
-        log("[bench] GEMM and Hadamard kernels")
+    if "gemm" in lines:
+        log("[bench] GEMM kernels")
         result["gemm"] = gemm_bench()
+    if "hadamard" in lines:
+        log("[bench] Hadamard kernel")
         result["hadamard"] = hadamard_bench()
     print(json.dumps(result), flush=True)
     return 0

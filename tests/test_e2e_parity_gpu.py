@@ -4,7 +4,7 @@ untethered CPU encode (``oracle.encode``) on the same seeded inputs.
 The CPU side receives only what the GPU side receives -- the weight, the
 captured ``X^T X`` sum and its count, the seeds -- plus the global scale the
 GPU's search picked (that search is pinned on its own in
-``test_gscale_gpu.py``).  It then runs the float64 Hessian preparation,
+``test_gscale.py``).  It then runs the float64 Hessian preparation,
 congruence, block LDL, regularisation and BlockLDLQ with the C oracle
 Viterbi on every 16-row block.  Nothing of the GPU run feeds the CPU
 recursion.
