@@ -55,9 +55,10 @@ HBM_PEAK_GBPS = 8000.0
 MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "f32": 157.3}
 # VALU issue-slot occupancy of viterbi_tiles_kernel by PMC (profiles/viterbi_tiles_kernel_microbench.md)
 VITERBI_VALU_ISSUE_FRAC_PMC = {"K2": 1.06, "K3": 0.94}
-# HBM bytes per tile of the Viterbi kernel (FETCH_SIZE x 2.00 + WRITE_SIZE x 1.00 per dispatch, calibrated on a
-# 4 GiB device copy; profiles/viterbi_tiles_kernel_microbench.md): mostly the traceback decision stream.
-VITERBI_HBM_BYTES_PER_TILE = 1.629e6
+# HBM bytes per tile of the Viterbi kernel by rate (FETCH_SIZE x 2.00 + WRITE_SIZE x 1.00 per dispatch, calibrated
+# on a 4 GiB device copy; K3/K4 over every dispatch of a 20-expert layer step, K2 from the microbench;
+# profiles/layer_encode_config5.md): mostly the traceback decision stream.
+VITERBI_HBM_BYTES_PER_TILE = {2: 1.631e6, 3: 1.633e6, 4: 0.816e6}
 # Same counters for the decode launches: 1.013 x their algorithmic bytes (profiles/decode_kernel_layer.md).
 DECODE_TRAFFIC_OVER_ALGORITHMIC = 1.013
 # Same counters at the bench's GEMM and Hadamard shapes (profiles/gemm_tn_kernels_expert_shapes.md,
@@ -884,7 +885,8 @@ def headline(lay: dict, warmup: int) -> dict:
             "peak": FP32_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
-            "traffic": round(VITERBI_HBM_BYTES_PER_TILE * mean_tiles),
+            "traffic": round(sum(VITERBI_HBM_BYTES_PER_TILE[int(k[1:])] * d["tiles"] for k, d in vit["by_rate"].items())
+                             / max(vit["launches"], 1)),
             "kernel": "viterbi_tiles_kernel",
             "algorithmic": f"{FLOPS_PER_EDGE} FP32 flops/edge x {int(EDGES_PER_WEIGHT)} edges/weight x 256 weights/tile "
                            f"x {mean_tiles:.1f} tiles/launch (mean over {vit['launches']} launches in the timed region)",

@@ -29,7 +29,8 @@ constexpr int kBM = 128, kBN = 128, kThreads = 256;
 
 // ---------------------------------------------------------------- FP32 path
 constexpr int kBK32 = 16;
-constexpr int kPad32 = 4;  // row pad of the [k][m] LDS tiles
+constexpr int kPad32 = 16;  // row pad of the [k][m] LDS tiles: rows 4 apart start 64 banks apart, so the
+                             // four k-rows of a fragment read hit distinct banks
 
 struct F32Chunk {
     float4 a[2], b[2];
@@ -155,28 +156,40 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
 }
 
 // ---------------------------------------------------------------- bf16 path
-// 256 x 256 tile of C per 512-thread workgroup (eight waves of 128 x 64:
-// 32 MFMA accumulators each), 64 k per stage.  Operands arrive k-major
-// ([k][m] in memory) but every MFMA fragment wants 8 consecutive k of one
-// m, so each thread loads an 8 k x 8 m unit with eight 16-byte loads,
-// transposes it in registers (v_perm on bf16 pairs) and writes eight
-// k-contiguous 16-byte rows to LDS; fragments are then single 16-byte LDS
-// reads.  LDS is double-buffered and the next stage's global loads are in
-// flight during the current stage's MFMAs: one barrier per stage.
-// With A == B (the Gram matrix X^T X) only tiles on and above the diagonal
-// run; off-diagonal tiles also add their transpose (float4 stores along m).
+// 256 x 256 tile of C per 512-thread workgroup: eight waves of 128 x 64
+// (thirty-two 16 x 16 x 32 MFMA accumulators each), 64 k per stage.
+// Operands arrive k-major ([k][m] in memory) and are copied to LDS as they
+// are: 64 k-rows of 256 columns per operand and stage, 16-byte chunks,
+// coalesced 512-byte row segments.  MFMA fragments want 8 consecutive k of
+// one column; gfx950's transposing LDS read (ds_read_b64_tr_b16) delivers
+// them: within each 16 lanes, lane a addresses the 4 columns 4 (a & 3) of
+// k-row a >> 2, and lane i receives column i of the 4 k-rows.  Two such
+// reads (k-rows 0..3 and 4..7 of the lane's k octet) make one fragment.
+// LDS rows are 256 + 32 bf16 (576 bytes), and the 16-byte chunk index of
+// every row in an odd group of eight rows is XORed with 2: the transposing
+// reads of 32 lanes and the 16-byte writes of 16 lanes then all hit distinct
+// banks.  LDS is double-buffered and the next stage's global loads are in
+// flight during the current stage's MFMAs: one barrier per stage.  With
+// A == B (the Gram matrix X^T X) only tiles on and above the diagonal run;
+// off-diagonal tiles also add their transpose (float4 stores along m).
 constexpr int kT16 = 256;
 constexpr int kBK16 = 64;
-constexpr int kRow16 = kBK16 + 8;  // LDS row: 64 k + 8 pad (bf16) = 144 B
+constexpr int kRow16 = kT16 + 32;  // LDS row: 256 columns + 32 pad (bf16) = 576 B
 constexpr int kThreads16 = 512;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 
-struct Bf16Unit {
-    u32x4 r[8];  // k-rows 8 ko + 0..7, columns 8 co + 0..7 (bf16 pairs)
+// physical element offset of (k-row r, column col) in one operand's LDS tile
+__device__ __forceinline__ int lds_pos(int r, int col) {
+    return r * kRow16 + ((((col >> 3) ^ (((r >> 3) & 1) << 1))) << 3) + (col & 7);
+}
+
+struct Bf16Stage {
+    u32x4 v[4];  // chunks t % 32 of k-rows t / 32 + 16 q, q = 0..3
 };
 
-// Eight k-rows of one 16-byte column group through a buffer resource that
+// Four 16-byte chunks of one operand's stage through a buffer resource that
 // ends at the last 16-byte group of valid columns of the stage's last row
 // (row min(K, k0 + 64) - 1): reads past it return zero (the K edge and the
 // last row's tail), so no load is predicated and nothing past the matrix is
@@ -184,27 +197,34 @@ struct Bf16Unit {
 // only feed rows or columns of C that are never stored.  `span` is the number
 // of columns from the tile's first column to the end of its valid 16-byte
 // groups.
-__device__ __forceinline__ void load_bf16(Bf16Unit& u, const uint16_t* P, int64_t k0, int64_t K, int64_t ld, int span,
-                                          int r0, int col) {
+__device__ __forceinline__ void load_stage(Bf16Stage& u, const uint16_t* P, int64_t k0, int64_t K, int64_t ld,
+                                           int span, int t) {
     const int64_t left = K - k0;
     const int rows = static_cast<int>(left < kBK16 ? left : kBK16);
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(P + k0 * ld), 0, ((rows - 1) * static_cast<int>(ld) + span) * 2, 0x00020000);
+    const int r0 = t >> 5, ch = t & 31;
 #pragma unroll
-    for (int r = 0; r < 8; ++r)
-        u.r[r] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, ((r0 + r) * static_cast<int>(ld) + col) * 2, 0, 0);
+    for (int q = 0; q < 4; ++q)
+        u.v[q] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, ((r0 + 16 * q) * static_cast<int>(ld) + 8 * ch) * 2, 0, 0);
 }
 
-// rows [8 co + e][8 ko .. 8 ko + 7] of the [column][k] LDS tile
-__device__ __forceinline__ void store_bf16(const Bf16Unit& u, uint16_t (*S)[kRow16], int co, int ko) {
+__device__ __forceinline__ void store_stage(const Bf16Stage& u, uint16_t* S, int t) {
+    const int r0 = t >> 5, ch = t & 31;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;  // high or low bf16 of each k-row word
-        u32x4 v;
-#pragma unroll
-        for (int kp = 0; kp < 4; ++kp) v[kp] = __builtin_amdgcn_perm(u.r[2 * kp + 1][e >> 1], u.r[2 * kp][e >> 1], sel);
-        *reinterpret_cast<u32x4*>(&S[8 * co + e][8 * ko]) = v;
-    }
+    for (int q = 0; q < 4; ++q) *reinterpret_cast<u32x4*>(S + lds_pos(r0 + 16 * q, 8 * ch)) = u.v[q];
+}
+
+// fragment of 16 columns col0 .. col0 + 15 and the lane's k octet kk + 8 (lane / 16)
+__device__ __forceinline__ bf16x8 fragment(const uint16_t* S, int kk, int col0, int lane) {
+    const int a = lane & 15, r = kk + 8 * (lane >> 4) + (a >> 2), col = col0 + 4 * (a & 3);
+    typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(S + lds_pos(r, col)));
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(S + lds_pos(r + 4, col)));
+    const i16x4 w[2] = {lo, hi};
+    bf16x8 f;
+    __builtin_memcpy(&f, w, sizeof(f));
+    return f;
 }
 
 template <bool SYM>
@@ -212,7 +232,7 @@ __global__ __launch_bounds__(kThreads16) void gemm_tn_bf16_kernel(float* __restr
                                                                   const uint16_t* __restrict__ B, int64_t M,
                                                                   int64_t N, int64_t K, int64_t lda, int64_t ldb,
                                                                   int64_t ldc, float alpha, int tiles_n) {
-    __shared__ __attribute__((aligned(16))) uint16_t S[2][2][kT16][kRow16];  // [buffer][operand][column][k]
+    __shared__ __attribute__((aligned(16))) uint16_t S[2][2][kBK16 * kRow16];  // [buffer][operand][k-row, column]
     // Workgroup i runs on XCD i % 8: give every XCD a contiguous run of the tile order below, so the
     // workgroups resident on one XCD at a time cover a compact 4 x 8 group of tiles and share 4 A and 8 B
     // operand panels in that XCD's L2.  Tile order: groups row-major, tiles row-major inside a group; with
@@ -245,12 +265,11 @@ found:
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int c = lane & 15, g = lane >> 4;
     const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
-    // staging unit of this thread: operand op (uniform per wave), column octet co, k octet ko
-    const int op = __builtin_amdgcn_readfirstlane(t >> 8), u = t & 255, co = u & 31, ko = u >> 5;
-    const uint16_t* P = op ? B + n0 : A + m0;
-    const int64_t pld = op ? ldb : lda, pcols = op ? N : M, pc0 = op ? n0 : m0;
-    const int64_t pend = ((pcols + 7) & ~int64_t{7}) < pld ? ((pcols + 7) & ~int64_t{7}) : pld;
-    const int span = static_cast<int>(pend - pc0);
+    const int64_t endA = ((M + 7) & ~int64_t{7}) < lda ? ((M + 7) & ~int64_t{7}) : lda;
+    const int64_t endB = ((N + 7) & ~int64_t{7}) < ldb ? ((N + 7) & ~int64_t{7}) : ldb;
+    const int spanA = static_cast<int>(endA - m0), spanB = static_cast<int>(endB - n0);
+    const uint16_t* PA = A + m0;
+    const uint16_t* PB = B + n0;
 
     f32x4 acc[8][4];
 #pragma unroll
@@ -259,10 +278,15 @@ found:
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int64_t stages = (K + kBK16 - 1) / kBK16;
-    Bf16Unit unit;
-    load_bf16(unit, P, 0, K, pld, span, 8 * ko, 8 * co);
-    store_bf16(unit, S[0][op], co, ko);
-    if (stages > 1) load_bf16(unit, P, kBK16, K, pld, span, 8 * ko, 8 * co);
+    Bf16Stage ua, ub;
+    load_stage(ua, PA, 0, K, lda, spanA, t);
+    load_stage(ub, PB, 0, K, ldb, spanB, t);
+    store_stage(ua, S[0][0], t);
+    store_stage(ub, S[0][1], t);
+    if (stages > 1) {
+        load_stage(ua, PA, kBK16, K, lda, spanA, t);
+        load_stage(ub, PB, kBK16, K, ldb, spanB, t);
+    }
     __syncthreads();
     for (int64_t s = 0; s < stages; ++s) {
         const int cur = static_cast<int>(s & 1);
@@ -270,17 +294,23 @@ found:
         for (int kk = 0; kk < kBK16; kk += 32) {
             bf16x8 a[8], b[4];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const bf16x8*>(&S[cur][0][wm + 16 * i + c][kk + 8 * g]);
+            for (int i = 0; i < 8; ++i) a[i] = fragment(S[cur][0], kk, wm + 16 * i, lane);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const bf16x8*>(&S[cur][1][wn + 16 * j + c][kk + 8 * g]);
+            for (int j = 0; j < 4; ++j) b[j] = fragment(S[cur][1], kk, wn + 16 * j, lane);
 #pragma unroll
             for (int i = 0; i < 8; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
         }
-        if (s + 1 < stages) store_bf16(unit, S[cur ^ 1][op], co, ko);
-        if (s + 2 < stages) load_bf16(unit, P, (s + 2) * kBK16, K, pld, span, 8 * ko, 8 * co);
+        if (s + 1 < stages) {
+            store_stage(ua, S[cur ^ 1][0], t);
+            store_stage(ub, S[cur ^ 1][1], t);
+        }
+        if (s + 2 < stages) {
+            load_stage(ua, PA, (s + 2) * kBK16, K, lda, spanA, t);
+            load_stage(ub, PB, (s + 2) * kBK16, K, ldb, spanB, t);
+        }
         __syncthreads();
     }
 
