@@ -760,7 +760,7 @@ def k2_expert_bench(reps: int = 2) -> dict:
             "proxy_err": {m: round(res[m]["proxy"], 5) for m in ("w1", "w3", "w2")}}
 
 
-def gemm_bench(steps: int = 5):
+def gemm_bench(steps: int = 20):
     """The two MFMA GEMM shapes of the config-4 expert encode:
     Hessian capture ``H += X^T X`` of 16,384 bf16 tokens x 7168 channels,
     and one LDLQ span update ``P[:begin] += L[span, :begin]^T (W - Q)[span]``

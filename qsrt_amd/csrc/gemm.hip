@@ -168,8 +168,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
 // LDS rows are 256 + 32 bf16 (576 bytes), and the 16-byte chunk index of
 // every row in an odd group of eight rows is XORed with 2: the transposing
 // reads of 32 lanes and the 16-byte writes of 16 lanes then all hit distinct
-// banks.  LDS is double-buffered and the next stage's global loads are in
-// flight during the current stage's MFMAs: one barrier per stage.  With
+// banks.  LDS is double-buffered; half-way through a stage each thread
+// writes the next stage to LDS and requests the one after, so global loads
+// have a stage and a half to land: one barrier per stage.  With
 // A == B (the Gram matrix X^T X) only tiles on and above the diagonal run;
 // off-diagonal tiles also add their transpose (float4 stores along m).
 constexpr int kT16 = 256;
@@ -302,14 +303,19 @@ found:
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-        }
-        if (s + 1 < stages) {
-            store_stage(ua, S[cur ^ 1][0], t);
-            store_stage(ub, S[cur ^ 1][1], t);
-        }
-        if (s + 2 < stages) {
-            load_stage(ua, PA, (s + 2) * kBK16, K, lda, spanA, t);
-            load_stage(ub, PB, (s + 2) * kBK16, K, ldb, spanB, t);
+            if (kk == 0) {
+                // Between the two halves of the stage (the other buffer is free since the last barrier): the
+                // next stage goes to LDS and the one after is requested, so the waves' store phases overlap
+                // the second half's MFMAs and the loads have a stage and a half to land.
+                if (s + 1 < stages) {
+                    store_stage(ua, S[cur ^ 1][0], t);
+                    store_stage(ub, S[cur ^ 1][1], t);
+                }
+                if (s + 2 < stages) {
+                    load_stage(ua, PA, (s + 2) * kBK16, K, lda, spanA, t);
+                    load_stage(ub, PB, (s + 2) * kBK16, K, ldb, spanB, t);
+                }
+            }
         }
         __syncthreads();
     }

@@ -76,6 +76,32 @@ def test_bf16_gram_matches_float64(n, k):
     assert _rel(Hf.cpu().double().numpy(), x64.T @ x64) < 1e-5
 
 
+def test_bf16_gram_full_size_matches_float64():
+    """The Hessian capture at the config-4 shape: 16,384 bf16 rows x 7168
+    channels.  Reference: the float64 product on the device (rocBLAS DGEMM),
+    itself pinned on 64 sampled entries by float64 dot products on the CPU."""
+
+    n, k = 16384, 7168
+    print(f"[gemm] bf16 gram full size n{n} k{k}", file=sys.stderr, flush=True)
+    g = torch.Generator(device="cuda").manual_seed(7168)
+    X = torch.randn(n, k, device="cuda", generator=g).bfloat16()
+    H = torch.zeros(k, k, device="cuda")
+    gemm.gram_(H, X, alpha=1.0 / n)
+    X64 = X.double()
+    ref = (X64.T @ X64) / n
+    del X64
+    scale = ref.abs().max().item()
+    assert (H.double() - ref).abs().max().item() / scale < 1e-5
+    rng = np.random.default_rng(5)
+    idx = rng.integers(0, k, size=(64, 2))
+    xc = X.cpu().double().numpy()
+    for i, j in idx:
+        exact = float(xc[:, i] @ xc[:, j]) / n
+        assert abs(ref[i, j].item() - exact) <= 1e-12 * scale
+        assert abs(H[i, j].item() - exact) <= 1e-5 * scale
+        assert H[i, j].item() == H[j, i].item()
+
+
 @pytest.mark.parametrize("K,M,N", [(1000, 520, 264), (64, 256, 256), (129, 8, 600)])
 def test_bf16_general_product_matches_float64(K, M, N):
     """Distinct operands take the full tile grid (no mirroring)."""
