@@ -37,6 +37,7 @@ import json
 import math
 import os
 import sys
+import tempfile
 import time
 from pathlib import Path
 from types import SimpleNamespace
@@ -419,23 +420,67 @@ def layer_bench(steps: int, warmup: int, experts: int = LAYER_EXPERTS):
             "proxy_mean": sum(proxies) / len(proxies), "proxy_max": max(proxies), "warm": warm, "counts": counts}
 
 
-def layer_decode(encoded: list, reps: int = 3) -> dict:
-    """Decode every packed matrix of the encoded layer to bf16 (one prepared
-    plan, one launch per rate), HIP events on the launch stream."""
+def layer_store(encoded: list, directory: str) -> dict:
+    """Write the encoded layer as a rate-record layer file (every expert's
+    atoms assembled on the GPU, written one expert at a time), read every
+    expert back and check the payloads and scales are the encoder's, byte
+    for byte.  Returns the file's facts and the read-back matrices (on the
+    GPU) for the decode."""
+
+    from qsrt_amd.qsrt import Geometry
+    from qsrt_amd.qsrt_rate_atoms import (SCHEMA, QSRTRateLayerLayout, QSRTRateLayerReader, RateSchedule,
+                                          materialize_rate_layer)
+
+    dev = torch.device("cuda:0")
+    sched = RateSchedule(Geometry(LAYER_INTER, LAYER_HIDDEN), LAYER_RECORD_BITS)
+    layout = QSRTRateLayerLayout(LAYER_ID, sched, tuple(e["expert"] for e in encoded))
+    path = Path(directory) / f"qsrt-layer-{LAYER_ID:05d}.safetensors"
+
+    def experts():
+        for e in encoded:
+            yield e["expert"], {m: {"trellis": e[m]["words"], "suh": e[m]["suh"], "svh": e[m]["svh"]}
+                                for m in ("w1", "w3", "w2")}
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    info = materialize_rate_layer(path, layout, experts())
+    t_write = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    mats, same = [], True
+    with QSRTRateLayerReader(path) as rd:
+        for e in encoded:
+            parts = rd.read_expert(e["expert"], device=dev)
+            for m in ("w1", "w3", "w2"):
+                p, r = parts[m], e[m]
+                same &= bool(torch.equal(p["trellis"], r["words"]) and torch.equal(p["suh"], r["suh"])
+                             and torch.equal(p["svh"], r["svh"]))
+                mats.append((p["trellis"], p["suh"], p["svh"], r["rate_axis"], r["shape"]))
+    torch.cuda.synchronize()
+    t_read = time.perf_counter() - t0
+    path.unlink()
+    if not same:
+        raise RuntimeError("the layer file did not read back as the encoder's payloads")
+    return {"facts": {"schema": SCHEMA, "experts": info["experts"], "disk_bytes": info["disk_bytes"],
+                      "payload_bytes": info["payload_bytes"], "write_s": round(t_write, 2),
+                      "read_s": round(t_read, 2), "read_back_equal": same}, "mats": mats}
+
+
+def layer_decode(mats: list, reps: int = 3) -> dict:
+    """Decode every packed matrix of the layer to bf16 (one prepared plan,
+    one launch per rate), HIP events on the launch stream.  ``mats``:
+    ``(record-major words, suh, svh, rate axis, (K, N))`` per matrix, on the
+    GPU."""
 
     from qsrt_amd.decode import DecodePlan
     from qsrt_amd.sqg_e4m3 import sqg_xor_cheb_t12_bytes
 
     dev = torch.device("cuda:0")
     payloads, outs = [], []
-    for e in encoded:
-        for m in ("w1", "w3", "w2"):
-            r = e[m]
-            k, n = r["shape"]
-            out = torch.empty((k, n), dtype=torch.bfloat16, device=dev)
-            outs.append(out)
-            payloads.append((r["words"], LAYER_RECORD_BITS, r["rate_axis"], (r["suh"].float() / 128.0).contiguous(),
-                             r["svh"].float().contiguous(), out))
+    for words, suh, svh, axis, (k, n) in mats:
+        out = torch.empty((k, n), dtype=torch.bfloat16, device=dev)
+        outs.append(out)
+        payloads.append((words, LAYER_RECORD_BITS, axis, (suh.float() / 128.0).contiguous(), svh.float().contiguous(),
+                         out))
     plan = DecodePlan.for_records(payloads, {b: sqg_xor_cheb_t12_bytes(b).to(dev) for b in set(LAYER_RECORD_BITS)})
     plan.run()
     torch.cuda.synchronize()
@@ -455,9 +500,9 @@ def layer_decode(encoded: list, reps: int = 3) -> dict:
     del plan, payloads, outs
     torch.cuda.empty_cache()
     return {
-        "workload": f"the encoded config-5 layer: {n_mat} packed matrices ({len(encoded)} experts x gate, up, down), "
-                    f"records {LAYER_RECORD_BITS.count(3)} K3 + {LAYER_RECORD_BITS.count(4)} K4 ({bpw:.3f} trellis bpw) "
-                    "-> bf16",
+        "workload": f"the stored config-5 layer read back from its layer file: {n_mat} packed matrices "
+                    f"({n_mat // 3} experts x gate, up, down), records {LAYER_RECORD_BITS.count(3)} K3 + "
+                    f"{LAYER_RECORD_BITS.count(4)} K4 ({bpw:.3f} trellis bpw) -> bf16",
         "kernel": "decode_kernel (one launch per rate)",
         "ms": round(t * 1e3, 3),
         "G_weights_per_s": round(weights / t / 1e9, 2),
@@ -941,8 +986,14 @@ def main() -> int:
         lay = layer_bench(args.steps, args.warmup, args.experts)
         result = headline(lay, args.warmup)
         value = result["value"]
-        log("[bench] decode of the encoded layer")
-        result["decode"] = layer_decode(lay["encoded"])
+        log("[bench] layer file: write, read back, compare")
+        with tempfile.TemporaryDirectory(prefix="qsrt-bench-") as tmp:
+            stored = layer_store(lay["encoded"], tmp)
+        log(f"[bench] layer file {json.dumps(stored['facts'])}")
+        log("[bench] decode of the stored layer")
+        result["decode"] = layer_decode(stored["mats"])
+        result["decode"]["layer_file"] = stored["facts"]
+        del stored
         log(f"[bench] decode {result['decode']['ms']} ms, {result['decode']['roofline']['achieved']} GB/s")
         first = next(e for e in lay["encoded"] if "encoded" in e["w1"])
         sample_src = expert_source(5, torch.device("cuda:0"), expert=first["expert"], tokens=first["tokens"])
