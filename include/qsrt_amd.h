@@ -72,6 +72,27 @@ int qsrt_viterbi_tiles_ex(const float *tiles, float *recon, uint16_t *states, in
                           void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * The reference extension's call shape, argument for argument:
+ * quantize_tiles_sqg(input_tiles, output_tiles, output_indices, temp_costs,
+ * temp_edges, codebook, K, tailbite_context, lut_abs_max)
+ * (qsrt/csrc/sqg_quantize.cpp:56-59 -> qsrt/csrc/sqg_quantize.cu:651-783),
+ * with each tensor as a device pointer (and byte size for the two
+ * temporaries), so the reference's own caller (qsrt/sqg_quantizer.py:
+ * 478-654) binds it unchanged.  `codebook` is what that caller passes: for
+ * K2..K4 its [out-edge pair][predecessor][2] transpose of the state-indexed
+ * E4M3 table (qsrt/sqg_quantizer.py:612-633), otherwise the table itself.
+ * The FP16 cost buffer is not needed here (costs live in LDS); its first
+ * 64 KiB receive the state-indexed table.  `temp_edges` is the traceback
+ * workspace and bounds how many compute units run at once.  The boundary
+ * rule follows the reference's kernel choice: K2 with a finite lut_abs_max
+ * in (0, 16] scores the last primer step, every other case the one before.
+ * Path metrics are FP32 with lowest-index ties (the reference's are FP16).
+ */
+int qsrt_quantize_tiles_sqg(const float *input_tiles, float *output_tiles, int16_t *output_indices, int64_t n_tiles,
+                            void *temp_costs, size_t temp_costs_bytes, uint8_t *temp_edges, size_t temp_edges_bytes,
+                            const uint8_t *codebook, int K, int tailbite_context, double lut_abs_max, void *stream);
+
+/*
  * EXL word packing of n_tiles tiles at rate K (1..6; the QSRT container uses
  * 2..4, the uniform codec paths of qsrt/qsrt_codec_pilot.py:220-281 up to 6):
  *   states u16 [n_tiles, 256] (only the low K bits are stored; 16-byte

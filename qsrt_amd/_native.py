@@ -40,6 +40,11 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_int, _c_int, _c_void_p, _c_int, _c_int, _c_void_p, _c_size,
          _c_void_p],
     ),
+    "qsrt_quantize_tiles_sqg": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p, _c_size, _c_void_p, _c_size, _c_void_p, _c_int, _c_int,
+         ctypes.c_double, _c_void_p],
+    ),
     "qsrt_pack_edges": (_c_int, [_c_void_p, _c_i64, _c_int, _c_void_p, _c_void_p]),
     "qsrt_unpack_states": (_c_int, [_c_void_p, _c_i64, _c_int, _c_void_p, _c_void_p]),
     "qsrt_decode_workspace_bytes": (_c_size, [_c_int]),

@@ -29,6 +29,8 @@
 //
 // Arithmetic contract (bit-exact with oracle/viterbi_ref.c): see that file.
 
+#include <cmath>
+
 #include "common.h"
 #include "qsrt_amd.h"
 
@@ -646,6 +648,18 @@ int launch_workgroups(int64_t n_tiles, int cu_count) {
     return static_cast<int>(g);
 }
 
+// The reference hands its kernels the K2..K4 codebook as [out-edge pair][predecessor][2] bytes
+// (qsrt/sqg_quantizer.py:612-633 transposes the state-indexed [predecessor][out-edge pair][2] table so that a
+// CUDA thread fetches all its predecessors' labels in one vector load).  This kernel writes the state-indexed
+// table back: state s = (p << (16 - K)) | (2 e + b) sits at transposed byte (e * 2^K + p) * 2 + b.
+__global__ __launch_bounds__(256) void untranspose_codebook_kernel(const uint8_t* __restrict__ transposed,
+                                                                   uint8_t* __restrict__ state_indexed, int K) {
+    const int s = blockIdx.x * 256 + threadIdx.x;
+    const int p = s >> (16 - K), rest = s & ((1 << (16 - K)) - 1);
+    const int e = rest >> 1, b = rest & 1;
+    state_indexed[s] = transposed[((e << K) + p) * 2 + b];
+}
+
 }  // namespace
 
 extern "C" {
@@ -702,5 +716,41 @@ int qsrt_viterbi_tiles_ex(const float* tiles, float* recon, uint16_t* states, in
     QSRT_HIP_TRY(hipGetLastError());
     return qsrt::kOk;
 }
+
+int qsrt_quantize_tiles_sqg(const float* input_tiles, float* output_tiles, int16_t* output_indices, int64_t n_tiles,
+                            void* temp_costs, size_t temp_costs_bytes, uint8_t* temp_edges, size_t temp_edges_bytes,
+                            const uint8_t* codebook, int K, int tailbite_context, double lut_abs_max,
+                            void* stream_handle) {
+    hipStream_t stream = static_cast<hipStream_t>(stream_handle);
+    if (K < 1 || K > 6) return qsrt::fail(qsrt::kBadArgument, "SQG validation kernel supports K1--K6");
+    if (tailbite_context < 1 || tailbite_context > 128)
+        return qsrt::fail(qsrt::kBadArgument, "tailbite_context must be in 1..128");
+    if (n_tiles < 0) return qsrt::fail(qsrt::kBadArgument, "n_tiles must be non-negative");
+    if (n_tiles == 0) return qsrt::kOk;
+    if (!input_tiles || !output_tiles || !output_indices || !temp_costs || !temp_edges || !codebook)
+        return qsrt::fail(qsrt::kBadArgument, "null pointer argument");
+    // the reference's K2 fast kernel (chosen for finite label bounds in (0, 16]) scores the last primer step,
+    // its generic kernel the one before (qsrt/csrc/sqg_quantize.cu:730-749)
+    const int lag = (K == 2 && std::isfinite(lut_abs_max) && lut_abs_max > 0.0 && lut_abs_max <= 16.0) ? 0 : 1;
+    const uint8_t* lut = codebook;
+    if (K >= 2 && K <= 4) {
+        // the FP16 cost buffer is not needed (costs live in LDS): its first 64 KiB hold the state-indexed table
+        if (temp_costs_bytes < 65536)
+            return qsrt::fail(qsrt::kWorkspaceTooSmall, "temp_costs must hold at least 65536 bytes");
+        uint8_t* table = static_cast<uint8_t*>(temp_costs);
+        hipLaunchKernelGGL(untranspose_codebook_kernel, dim3(256), dim3(256), 0, stream, codebook, table, K);
+        QSRT_HIP_TRY(hipGetLastError());
+        lut = table;
+    }
+    // the traceback buffer bounds how many workgroups run at once
+    const size_t per = workgroup_dec_bytes(K);
+    if (temp_edges_bytes < per)
+        return qsrt::fail(qsrt::kWorkspaceTooSmall, "temp_edges too small: %zu < %zu bytes", temp_edges_bytes, per);
+    const size_t fit = temp_edges_bytes / per;
+    const int cap = fit > 0x7fffffff ? 0x7fffffff : static_cast<int>(fit);
+    return qsrt_viterbi_tiles_ex(input_tiles, output_tiles, reinterpret_cast<uint16_t*>(output_indices), n_tiles, K,
+                                 tailbite_context, lut, lag, cap, temp_edges, temp_edges_bytes, stream_handle);
+}
+
 
 }  // extern "C"
