@@ -16,7 +16,8 @@ resolved the other way, and its squared error must be within 1e-6 relative
 of the CPU path's on the CPU target.  The tile mismatch rate is printed.
 Tiles above such a tile in the same column see a different target (the
 feedback runs along columns), so they are counted but not held to the tie
-bar; their effect is bounded through the proxy error.
+bar; their effect is bounded through the proxy error, and the near-tie
+events themselves must stay rare (at most one per 256 tiles, or one).
 """
 
 from __future__ import annotations
@@ -64,6 +65,16 @@ def _gpu_encode(W: torch.Tensor, H_sum: torch.Tensor, count: int, bits: int, see
     return weight_q, proxy, tensors, qa, shared
 
 
+def _check_tie_events(name: str, stats: dict) -> None:
+    """Near-tie events stay rare.  Each one is held to the SSE bar above;
+    the tiles above it in its column then see other targets and may differ
+    too (they are counted in the mismatch rate, and bounded through the
+    proxy error), so the bound is on events, not on differing tiles."""
+
+    events = len(stats["first"])
+    assert events <= max(1, stats["tiles"] // 256), f"{name}: {events} near-tie events in {stats['tiles']} tiles"
+
+
 def _check_matrix(name: str, W: torch.Tensor, H_sum: torch.Tensor, count: int, bits: int, seeds) -> dict:
     k, n = W.shape
     _say(f"[e2e] {name}: [{k} x {n}] K{bits} on cuda:0")
@@ -99,7 +110,7 @@ def _check_matrix(name: str, W: torch.Tensor, H_sum: torch.Tensor, count: int, b
     for d in deltas:
         assert d <= TIE_SSE_REL, f"{name}: a differing tile's SSE is {d:.3e} relative from the CPU path's"
     assert abs(proxy - cpu_proxy) <= 1e-3 * cpu_proxy
-    assert stats["mismatch_rate"] <= 0.01
+    _check_tie_events(name, stats)
     return stats
 
 
@@ -198,4 +209,6 @@ def test_batch_conditioned_path_matches_cpu_encode():
              f"{oenc.proxy(cpu['W_r'], cpu['Q'], cpu['H_c']):.6f}")
         for dlt in deltas:
             assert dlt <= TIE_SSE_REL
-        assert stats["mismatch_rate"] <= 0.01
+        cpu_proxy = oenc.proxy(cpu["W_r"], cpu["Q"], cpu["H_c"])
+        assert abs(res[0]["proxy"] - cpu_proxy) <= 5e-3 * cpu_proxy
+        _check_tie_events(f"batch {matrix}", stats)
