@@ -525,7 +525,7 @@ def _sign_draw(n: int, seed: int):
     return (torch.randn(n, generator=g).sign() + 1e-5).sign().double().numpy()
 
 
-def layer_cpu_sample(first: dict, source: dict, blocks: int = 24) -> dict:
+def layer_cpu_sample(first: dict, source: dict, blocks: int = 96) -> dict:
     """The CPU oracle on the layer's first expert, w1, over the bottom
     ``blocks`` 16-row blocks -- the first steps of the backward recursion,
     which depend on nothing above them.  Two comparisons with the GPU's
@@ -590,8 +590,8 @@ def layer_cpu_sample(first: dict, source: dict, blocks: int = 24) -> dict:
         "cpu": {"value": round(n_w / t_rec / 1e6, 5), "unit": "M weights/s", "cores": threads, "kind": "port",
                 "sample": f"expert 0 w1 of the layer ({source['tokens']} routed rows), the bottom {blocks} of {kt} "
                           f"16-row blocks ({blocks * nt} tiles, {n_w} weights): the float64 BlockLDLQ of "
-                          f"oracle/encode.py with oracle/viterbi_ref.c on {threads} OpenMP threads at the layer's "
-                          f"record rates; the Hessian preparation and factorisation ({t_prep:.1f} s per matrix in "
+                          f"oracle/encode.py with oracle/viterbi_ref.c (AVX2) on {threads} OpenMP threads at the "
+                          f"layer's record rates; the Hessian preparation and factorisation ({t_prep:.1f} s per matrix in "
                           "float64) and the global-scale search (about 22% more tile encodes on the GPU) are not "
                           "charged, so the CPU rate is an upper bound",
                 "seconds": round(t_rec, 2)},
@@ -696,7 +696,7 @@ def microbench_cpu(bits: int = 3, seconds: float = 6.0) -> dict:
         n += len(tiles)
     per_tile = (time.perf_counter() - t0) / n
     return {"value": round(256 / per_tile / 1e6, 4), "unit": "M weights/s", "cores": threads, "ms_per_tile": per_tile * 1e3,
-            "sample": f"{n} microbench tiles at K{bits}, oracle/viterbi_ref.c with {threads} OpenMP threads"}
+            "sample": f"{n} microbench tiles at K{bits}, oracle/viterbi_ref.c (AVX2) with {threads} OpenMP threads"}
 
 
 def expert_bench(bits: int = 3, reps: int = 2) -> dict:

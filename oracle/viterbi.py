@@ -50,8 +50,17 @@ def _load():
             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
             ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
         ]
+        lib.qsrt_oracle_set_vector.restype = None
+        lib.qsrt_oracle_set_vector.argtypes = [ctypes.c_int]
         _lib = lib
     return _lib
+
+
+def set_vector(enable: bool) -> None:
+    """Select the AVX2 path (default) or the scalar path of the C oracle;
+    both compute the same values bit for bit."""
+
+    _load().qsrt_oracle_set_vector(1 if enable else 0)
 
 
 def encode(

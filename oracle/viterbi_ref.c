@@ -1,5 +1,5 @@
 /*
- * Oracle: tail-biting tile Viterbi in plain FP32 C -- TEST INFRASTRUCTURE ONLY.
+ * Oracle: tail-biting tile Viterbi in FP32 C -- TEST INFRASTRUCTURE ONLY.
  *
  * CPU restatement of the reference's tile quantizer pass structure
  * (qsrt/csrc/qsrt_quantize_tiles_kernel.cuh:79-499 and
@@ -15,7 +15,10 @@
  *   per-state choice: lowest predecessor index k among equal minima
  *   boundary choice:  lowest state index among equal minima
  *   unreachable edges carry +inf (constrained first step only).
- * Built with -ffp-contract=off and without fast-math.
+ * Built with -ffp-contract=off and without fast-math.  Steps after the first
+ * run on AVX2 (sixteen states at a time, the same operations per lane); the
+ * scalar loop below is the definition and a test compares the two bit for
+ * bit.
  *
  * Trellis: codeword w has L bits; state = w & (2^(L-K) - 1); the codeword
  * entering state s from predecessor choice k is (k << (L-K)) | s and that
@@ -38,6 +41,9 @@
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+#ifdef __AVX2__
+#include <immintrin.h>
+#endif
 
 #ifdef _OPENMP
 #include <omp.h>
@@ -48,6 +54,70 @@ typedef struct {
     float *a, *b;      /* cost ping-pong, S floats each */
     uint8_t *dec;      /* T * S decisions */
 } vt_ctx;
+
+/* The vector path (AVX2 + FMA, sixteen consecutive states at a time) computes
+ * exactly the scalar path's values: the same subtract, one fused multiply-add
+ * per edge, and a strict less-than that keeps the lowest predecessor index on
+ * ties (and, like the scalar compare, never replaces a value by a NaN).
+ * qsrt_oracle_set_vector(0) selects the scalar path (tests compare the two). */
+static int vt_use_vector = 1;
+
+void qsrt_oracle_set_vector(int enable) { vt_use_vector = enable != 0; }
+
+#ifdef __AVX2__
+/* predecessor costs of states s0 .. s0+7 (s0 a multiple of 8) for choice k */
+static inline __m256 vt_pred8(const float *prev, int k, int q0, int K, int pred_shift)
+{
+    const float *pp = prev + (k << pred_shift) + q0;
+    if (K >= 3) return _mm256_set1_ps(pp[0]);
+    if (K == 2) return _mm256_set_m128(_mm_set1_ps(pp[1]), _mm_set1_ps(pp[0]));
+    return _mm256_setr_ps(pp[0], pp[0], pp[1], pp[1], pp[2], pp[2], pp[3], pp[3]);
+}
+
+static inline void vt_store_dec8(uint8_t *drow, int s0, __m256i arg)
+{
+    /* eight decisions (< 64) narrowed to bytes */
+    const __m128i h = _mm_packs_epi32(_mm256_castsi256_si128(arg), _mm256_extracti128_si256(arg, 1));
+    _mm_storel_epi64((__m128i *)(drow + s0), _mm_packus_epi16(h, h));
+}
+
+/* costs of the 16 states s0 .. s0+15 (s0 a multiple of 16) at a step after the
+ * first: two independent groups of eight, so the compare/blend chains of the
+ * two overlap */
+static void vt_step16(const float *lab, const float *prev, float *next, uint8_t *drow, int record, float w, int s0,
+                      int K, int P, int word_shift, int pred_shift)
+{
+    const __m256 wv = _mm256_set1_ps(w);
+    const int qa = s0 >> K, qb = (s0 + 8) >> K;
+    __m256 best_a = _mm256_setzero_ps(), best_b = _mm256_setzero_ps();
+    __m256i arg_a = _mm256_setzero_si256(), arg_b = _mm256_setzero_si256();
+    for (int k = 0; k < P; ++k) {
+        const float *lk = lab + ((size_t)k << word_shift) + s0;
+        const __m256 da = _mm256_sub_ps(_mm256_loadu_ps(lk), wv);
+        const __m256 db = _mm256_sub_ps(_mm256_loadu_ps(lk + 8), wv);
+        const __m256 ca = _mm256_fmadd_ps(da, da, vt_pred8(prev, k, qa, K, pred_shift));
+        const __m256 cb = _mm256_fmadd_ps(db, db, vt_pred8(prev, k, qb, K, pred_shift));
+        if (k == 0) {
+            best_a = ca;
+            best_b = cb;
+        } else {
+            const __m256 kv = _mm256_castsi256_ps(_mm256_set1_epi32(k));
+            const __m256 lta = _mm256_cmp_ps(ca, best_a, _CMP_LT_OQ);
+            const __m256 ltb = _mm256_cmp_ps(cb, best_b, _CMP_LT_OQ);
+            best_a = _mm256_blendv_ps(best_a, ca, lta);
+            best_b = _mm256_blendv_ps(best_b, cb, ltb);
+            arg_a = _mm256_castps_si256(_mm256_blendv_ps(_mm256_castsi256_ps(arg_a), kv, lta));
+            arg_b = _mm256_castps_si256(_mm256_blendv_ps(_mm256_castsi256_ps(arg_b), kv, ltb));
+        }
+    }
+    _mm256_storeu_ps(next + s0, best_a);
+    _mm256_storeu_ps(next + s0 + 8, best_b);
+    if (record) {
+        vt_store_dec8(drow, s0, arg_a);
+        vt_store_dec8(drow, s0 + 8, arg_b);
+    }
+}
+#endif
 
 /* One forward pass; returns the buffer holding the final costs and, via
  * *penult, the buffer holding the costs one step earlier. */
@@ -62,6 +132,16 @@ static float *vt_forward(vt_ctx *c, const float *lab, const float *x, int roll, 
         const float w = x[pos];
         const int record = i >= trace_start;
         uint8_t *drow = c->dec + (size_t)pos * S;
+#ifdef __AVX2__
+        if (i > 0 && vt_use_vector && S % 16 == 0) {
+            for (int s0 = 0; s0 < S; s0 += 16)
+                vt_step16(lab, prev, next, drow, record, w, s0, K, P, word_shift, pred_shift);
+            float *t = prev;
+            prev = next;
+            next = t;
+            continue;
+        }
+#endif
         for (int s = 0; s < S; ++s) {
             const int q = s >> K;
             float best = 0.0f;

@@ -96,3 +96,33 @@ def test_trellis_beats_scalar_at_k2():
     mse = float(((recon * scale - x) ** 2).mean())
     assert mse < 0.85 * 0.1175
     assert 0.060 < mse < 0.075
+
+
+@pytest.mark.parametrize("K", (1, 2, 3, 4, 5, 6))
+def test_vector_path_equals_scalar_path(K):
+    """The oracle's AVX2 path against its scalar path, bit for bit, at
+    production size (L = 16, C = 128) and on a tiny trellis, both boundary
+    rules, with saturated and tied inputs mixed in."""
+
+    rng = np.random.default_rng(40 + K)
+    lab = otables.t12_values(K) if K in (1, 2, 3, 4, 5, 6) else None
+    tiles = rng.standard_normal((6, 256)).astype(np.float32)
+    tiles[1] = 0.0  # every label equally far from x: ties everywhere
+    tiles[2] = 1e6  # saturated costs
+    small_lab = rng.integers(-3, 4, size=1 << 8).astype(np.float32)
+    small = rng.integers(-4, 5, size=(3, 12)).astype(np.float32)
+    for lag in (0, 1):
+        out = []
+        for vector in (True, False):
+            ov.set_vector(vector)
+            try:
+                out.append((ov.encode(tiles, lab, K=K, context=128, boundary_lag=lag, threads=2),
+                            ov.encode(small, small_lab, K=min(K, 4), L=8, context=4, boundary_lag=lag, threads=1)
+                            if 2 * min(K, 4) <= 8 else None))
+            finally:
+                ov.set_vector(True)
+        (big_v, small_v), (big_s, small_s) = out
+        assert np.array_equal(big_v[0].view(np.uint32), big_s[0].view(np.uint32))
+        assert np.array_equal(big_v[1], big_s[1])
+        if small_v is not None:
+            assert np.array_equal(small_v[1], small_s[1])
