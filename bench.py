@@ -609,11 +609,14 @@ def layer_cpu_sample(first: dict, source: dict, blocks: int = 96) -> dict:
 # ---------------------------------------------------------------------------
 
 
-def _time_ms(fn, steps: int, min_ms: float = 2.0) -> float:
+def _time_ms(fn, steps: int, min_ms: float = 2.0, warm_ms: float = 100.0) -> float:
     """Mean duration of ``fn`` over at least ``steps`` launches, HIP events on
     the current stream (the stream the kernels are launched on).  Short
     kernels get enough launches to fill ``min_ms`` of GPU time, so the mean
-    is the kernel's own duration rather than launch latency."""
+    is the kernel's own duration rather than launch latency; about
+    ``warm_ms`` of untimed launches come first, so the clocks have left
+    their idle state (the first ~20 launches of a 1 ms kernel after an idle
+    gap run up to 40% slower)."""
 
     fn()
     torch.cuda.synchronize()
@@ -622,7 +625,11 @@ def _time_ms(fn, steps: int, min_ms: float = 2.0) -> float:
     fn()
     e1.record()
     torch.cuda.synchronize()
-    reps = max(steps, min(2000, math.ceil(min_ms / max(e0.elapsed_time(e1), 1e-3))))
+    one = max(e0.elapsed_time(e1), 1e-3)
+    for _ in range(min(500, math.ceil(warm_ms / one))):
+        fn()
+    torch.cuda.synchronize()
+    reps = max(steps, min(2000, math.ceil(min_ms / one)))
     e0.record()
     for _ in range(reps):
         fn()

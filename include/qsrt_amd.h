@@ -231,6 +231,27 @@ int qsrt_gemm_tn(float *C, const void *A, const void *B, const void *B2, int64_t
                  int64_t lda, int64_t ldb, int64_t ldc, float alpha, int dtype, void *stream);
 
 /*
+ * Device bytes qsrt_gemm_tn_ws wants as workspace for these arguments (0 when
+ * the call has nothing to split: dtype 0, or a bf16 tile count that fills the
+ * device's compute units in whole rounds).
+ */
+size_t qsrt_gemm_tn_workspace_bytes(const float *C, const void *A, const void *B, int64_t M, int64_t N, int64_t K,
+                                    int64_t lda, int64_t ldb, int64_t ldc, int dtype);
+
+/*
+ * qsrt_gemm_tn with a device workspace (16-byte aligned).  bf16: when the
+ * 256 x 256 tiles do not fill the compute units in whole rounds, the tiles of
+ * the last round are split along K and their partial products, written to
+ * the workspace, are added to C in K order by a second kernel on the same
+ * stream (the result is deterministic; it differs from the unsplit sum only
+ * by FP32 rounding).  A NULL or short workspace runs every tile whole, as
+ * qsrt_gemm_tn does.  Same operator and call sites as qsrt_gemm_tn.
+ */
+int qsrt_gemm_tn_ws(float *C, const void *A, const void *B, const void *B2, int64_t M, int64_t N, int64_t K,
+                    int64_t lda, int64_t ldb, int64_t ldc, float alpha, int dtype, void *workspace,
+                    size_t workspace_bytes, void *stream);
+
+/*
  * BlockLDLQ step, batched over B members (member m quantizes source
  * src[m]).  For the 16-row block [blk, blk + 16) of a span ending at row
  * `end`, every member's target

@@ -173,6 +173,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
 // have a stage and a half to land: one barrier per stage.  With
 // A == B (the Gram matrix X^T X) only tiles on and above the diagonal run;
 // off-diagonal tiles also add their transpose (float4 stores along m).
+// One workgroup per CU (the LDS buffers take 144 KiB), so a tile count that
+// is not a multiple of the CU count leaves CUs idle in the last round (the
+// 406 Gram tiles of 7168 channels: 150 tiles in a second round on 256 CUs);
+// given a workspace, those tiles are split along K (bf16_plan below).
 constexpr int kT16 = 256;
 constexpr int kBK16 = 64;
 constexpr int kRow16 = kT16 + 32;  // LDS row: 256 columns + 32 pad (bf16) = 576 B
@@ -228,57 +232,63 @@ __device__ __forceinline__ bf16x8 fragment(const uint16_t* S, int kk, int col0, 
     return f;
 }
 
-template <bool SYM>
-__global__ __launch_bounds__(kThreads16) void gemm_tn_bf16_kernel(float* __restrict__ C, const uint16_t* __restrict__ A,
-                                                                  const uint16_t* __restrict__ B, int64_t M,
-                                                                  int64_t N, int64_t K, int64_t lda, int64_t ldb,
-                                                                  int64_t ldc, float alpha, int tiles_n) {
-    __shared__ __attribute__((aligned(16))) uint16_t S[2][2][kBK16 * kRow16];  // [buffer][operand][k-row, column]
-    // Workgroup i runs on XCD i % 8: give every XCD a contiguous run of the tile order below, so the
-    // workgroups resident on one XCD at a time cover a compact 4 x 8 group of tiles and share 4 A and 8 B
-    // operand panels in that XCD's L2.  Tile order: groups row-major, tiles row-major inside a group; with
-    // SYM only tiles on or above the diagonal exist.
-    const unsigned nwg = gridDim.x, xcd = blockIdx.x % 8u, per = nwg / 8u, rem = nwg % 8u;
-    int rest = static_cast<int>(xcd * per + (xcd < rem ? xcd : rem) + blockIdx.x / 8u);
+// Tile order: groups of 4 x 8 tiles, groups row-major, tiles row-major inside a group; with SYM only tiles
+// on or above the diagonal exist.  Returns false past the last tile.
+__device__ __forceinline__ bool tile_at(int idx, int tiles_m, int tiles_n, bool sym, int& tm, int& tn) {
     constexpr int GM = 4, GN = 8;
-    const int tiles_m = static_cast<int>((M + kT16 - 1) / kT16);
-    int tm = 0, tn = 0;
+    int rest = idx;
     for (int gr = 0; gr * GM < tiles_m; ++gr) {
-        for (int gc = 0; gc * GN < tiles_n; ++gc) {
+        // a whole group row at once: tiles of its rows (with SYM, columns from the row's own onwards)
+        int row_tiles = 0;
+        for (int i = 0; i < GM && gr * GM + i < tiles_m; ++i)
+            row_tiles += sym ? (tiles_n > gr * GM + i ? tiles_n - (gr * GM + i) : 0) : tiles_n;
+        if (rest >= row_tiles) {
+            rest -= row_tiles;
+            continue;
+        }
+        for (int gc = 0; gc * GN < tiles_n; ++gc)
             for (int i = 0; i < GM && gr * GM + i < tiles_m; ++i) {
                 const int row = gr * GM + i;
-                int lo = gc * GN, hi = gc * GN + GN < tiles_n ? gc * GN + GN : tiles_n;
-                if (SYM && lo < row) lo = row;
+                int lo = gc * GN;
+                const int hi = gc * GN + GN < tiles_n ? gc * GN + GN : tiles_n;
+                if (sym && lo < row) lo = row;
                 const int cnt = hi > lo ? hi - lo : 0;
                 if (rest < cnt) {
                     tm = row;
                     tn = lo + rest;
-                    goto found;
+                    return true;
                 }
                 rest -= cnt;
             }
-        }
+        return false;  // not reached: the group row holds the tile
     }
-    return;  // not reached: the grid holds exactly the tiles of the order
-found:
-    const int64_t m0 = static_cast<int64_t>(tm) * kT16, n0 = static_cast<int64_t>(tn) * kT16;
+    return false;
+}
 
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int c = lane & 15, g = lane >> 4;
+// Workgroup q of a range of n runs on XCD q % 8: it takes slot xcd_slot(q, n), so every XCD owns a
+// contiguous run of the range and the workgroups resident on one XCD at a time share operand panels
+// (a 4 x 8 group: 4 A and 8 B panels) in that XCD's L2.
+__device__ __forceinline__ int xcd_slot(int q, int n) {
+    const int x = q % 8, per = n / 8, rem = n % 8;
+    return x * per + (x < rem ? x : rem) + q / 8;
+}
+
+typedef uint16_t Bf16Lds[2][2][kBK16 * kRow16];  // [buffer][operand][k-row, column]
+
+// acc += A[k0 .. k1)^T B[k0 .. k1) over the tile's columns m0 .. m0 + 255 of A and n0 .. n0 + 255 of B
+__device__ __forceinline__ void bf16_mainloop(f32x4 (&acc)[8][4], Bf16Lds& S, const uint16_t* __restrict__ A,
+                                              const uint16_t* __restrict__ B, int64_t M, int64_t N, int64_t k0,
+                                              int64_t k1, int64_t lda, int64_t ldb, int64_t m0, int64_t n0, int t) {
+    const int lane = t & 63, wave = t >> 6;
     const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
     const int64_t endA = ((M + 7) & ~int64_t{7}) < lda ? ((M + 7) & ~int64_t{7}) : lda;
     const int64_t endB = ((N + 7) & ~int64_t{7}) < ldb ? ((N + 7) & ~int64_t{7}) : ldb;
     const int spanA = static_cast<int>(endA - m0), spanB = static_cast<int>(endB - n0);
-    const uint16_t* PA = A + m0;
-    const uint16_t* PB = B + n0;
-
-    f32x4 acc[8][4];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
+    const uint16_t* PA = A + k0 * lda + m0;
+    const uint16_t* PB = B + k0 * ldb + n0;
+    const int64_t K = k1 - k0;
     const int64_t stages = (K + kBK16 - 1) / kBK16;
+    if (stages <= 0) return;
     Bf16Stage ua, ub;
     load_stage(ua, PA, 0, K, lda, spanA, t);
     load_stage(ub, PB, 0, K, ldb, spanB, t);
@@ -319,40 +329,209 @@ found:
         }
         __syncthreads();
     }
+}
 
-    // lane holds C[m0 + wm + 16 i + 4 g + r][n0 + wn + 16 j + c], r = 0..3
+// C tile (tm, tn) += alpha * acc over the 16-row blocks i0 .. i0 + IB - 1 of every wave's 128 x 64 block;
+// with SYM an off-diagonal tile also adds its transpose.
+// lane holds C[m0 + wm + 16 i + 4 g + r][n0 + wn + 16 j + c], r = 0..3
+template <bool SYM, int IB>
+__device__ __forceinline__ void bf16_epilogue(float* __restrict__ C, const f32x4 (&acc)[IB][4], int i0, int64_t M,
+                                              int64_t N, int64_t ldc, float alpha, int tm, int tn, int t) {
+    const int lane = t & 63, wave = t >> 6, c = lane & 15, g = lane >> 4;
+    const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
+    const int64_t m0 = static_cast<int64_t>(tm) * kT16, n0 = static_cast<int64_t>(tn) * kT16;
+    if (m0 + kT16 <= M && n0 + kT16 <= N) {
+        // Interior tile: no per-element bounds, so the C loads of a 16-row block (and of its transposed
+        // block) are issued together and waited for once, not one load round trip per element.
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int64_t row0 = m0 + wm + 16 * i + 4 * g;
+        for (int ii = 0; ii < IB; ++ii) {
+            const int64_t row0 = m0 + wm + 16 * (i0 + ii) + 4 * g;
+            float v[4][4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[j][r] = C[(row0 + r) * ldc + n0 + wn + 16 * j + c];
+            f32x4 w[4];
+            if (SYM && tm != tn) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    w[j] = *reinterpret_cast<const f32x4*>(C + (n0 + wn + 16 * j + c) * ldc + row0);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    C[(row0 + r) * ldc + n0 + wn + 16 * j + c] = v[j][r] + alpha * acc[ii][j][r];
+            if (SYM && tm != tn) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    *reinterpret_cast<f32x4*>(C + (n0 + wn + 16 * j + c) * ldc + row0) = w[j] + alpha * acc[ii][j];
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int ii = 0; ii < IB; ++ii) {
+        const int64_t row0 = m0 + wm + 16 * (i0 + ii) + 4 * g;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int64_t col = n0 + wn + 16 * j + c;
             if (col >= N) continue;
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                if (row0 + r < M) C[(row0 + r) * ldc + col] += alpha * acc[i][j][r];
+                if (row0 + r < M) C[(row0 + r) * ldc + col] += alpha * acc[ii][j][r];
             if (SYM && tm != tn) {  // the transposed tile: C[col][row0 .. row0 + 3]
                 float* q = C + col * ldc + row0;
                 if (row0 + 3 < M) {
                     f32x4 v = *reinterpret_cast<const f32x4*>(q);
-                    v += alpha * acc[i][j];
+                    v += alpha * acc[ii][j];
                     *reinterpret_cast<f32x4*>(q) = v;
                 } else {
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        if (row0 + r < M) q[r] += alpha * acc[i][j][r];
+                        if (row0 + r < M) q[r] += alpha * acc[ii][j][r];
                 }
             }
         }
     }
 }
 
+// One partial of a split tile in the workspace: 32 accumulators x 512 threads x 16 bytes, accumulator-major
+// so a wave's stores and loads are contiguous.
+constexpr int64_t kPartialVec = 32 * kThreads16;  // f32x4 per partial (256 KiB)
+
+// Workgroups [0, dp) each own a whole tile: order[xcd_slot(b, dp)].  When the tile count is not a multiple
+// of the CU count, the tiles order[dp .. dp + sk) of the last, partial round are instead split into `parts`
+// K ranges and the workgroups [dp, dp + sk * parts) compute one range each into the workspace, range-major
+// (all first ranges, then all second ranges, ...), so the workgroups resident on one XCD at a time walk the
+// same K range of neighbouring tiles; gemm_tn_bf16_fixup adds the ranges to C in K order.
+template <bool SYM>
+__global__ __launch_bounds__(kThreads16) void gemm_tn_bf16_kernel(float* __restrict__ C, const uint16_t* __restrict__ A,
+                                                                  const uint16_t* __restrict__ B, int64_t M,
+                                                                  int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                                                                  int64_t ldc, float alpha, int tiles_n, int dp,
+                                                                  int sk, int parts, f32x4* __restrict__ ws) {
+    __shared__ __attribute__((aligned(16))) Bf16Lds S;
+    const int b = static_cast<int>(blockIdx.x), t = static_cast<int>(threadIdx.x);
+    const int tiles_m = static_cast<int>((M + kT16 - 1) / kT16);
+    f32x4 acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    int tm = 0, tn = 0;
+    if (b < dp) {
+        if (!tile_at(xcd_slot(b, dp), tiles_m, tiles_n, SYM, tm, tn)) return;  // not reached: dp <= tiles
+        bf16_mainloop(acc, S, A, B, M, N, 0, K, lda, ldb, static_cast<int64_t>(tm) * kT16,
+                      static_cast<int64_t>(tn) * kT16, t);
+        bf16_epilogue<SYM, 8>(C, acc, 0, M, N, ldc, alpha, tm, tn, t);
+        return;
+    }
+    const int q = xcd_slot(b - dp, sk * parts), part = q / sk, s = q % sk;
+    if (!tile_at(dp + s, tiles_m, tiles_n, SYM, tm, tn)) return;  // not reached
+    const int64_t stages = (K + kBK16 - 1) / kBK16;
+    const int64_t k0 = stages * part / parts * kBK16, k1 = stages * (part + 1) / parts * kBK16;
+    bf16_mainloop(acc, S, A, B, M, N, k0, k1 < K ? k1 : K, lda, ldb, static_cast<int64_t>(tm) * kT16,
+                  static_cast<int64_t>(tn) * kT16, t);
+    f32x4* w = ws + static_cast<int64_t>(part * sk + s) * kPartialVec;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[(i * 4 + j) * kThreads16 + t] = acc[i][j];
+}
+
+// Eight workgroups per split tile, one per 16-row block i of every wave's 128 x 64 block: the tile's K
+// ranges summed in K order, then the epilogue of those rows (and of their transpose).
+template <bool SYM>
+__global__ __launch_bounds__(kThreads16) void gemm_tn_bf16_fixup(float* __restrict__ C, int64_t M, int64_t N,
+                                                                 int64_t ldc, float alpha, int tiles_n, int dp,
+                                                                 int sk, int parts,
+                                                                 const f32x4* __restrict__ ws) {
+    const int s = static_cast<int>(blockIdx.x) / 8, i = static_cast<int>(blockIdx.x) % 8;
+    const int t = static_cast<int>(threadIdx.x);
+    int tm = 0, tn = 0;
+    if (!tile_at(dp + s, static_cast<int>((M + kT16 - 1) / kT16), tiles_n, SYM, tm, tn)) return;  // not reached
+    const f32x4* w = ws + static_cast<int64_t>(s) * kPartialVec;
+    f32x4 acc[1][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[0][j] = w[(i * 4 + j) * kThreads16 + t];
+    for (int part = 1; part < parts; ++part) {
+        const f32x4* wp = w + static_cast<int64_t>(part) * sk * kPartialVec;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[0][j] += wp[(i * 4 + j) * kThreads16 + t];
+    }
+    bf16_epilogue<SYM, 1>(C, acc, i, M, N, ldc, alpha, tm, tn, t);
+}
+
+// Launch plan of the bf16 path: `tiles` tiles on `cus` compute units.  A last round that would leave CUs
+// idle is split along K into `parts` ranges, chosen to minimise (rounds of ranges) / parts + 0.09 x
+// (ranges per CU) in units of one tile's time: the first term is the split round's length, the second the
+// cost of writing and re-reading each range's partial (fitted on MI355X to the Gram of a 16384 x 7168
+// operand at 2, 3, 4, 5 and 8 parts; 3 parts there, 8 for the 28 x 28 tiles of the full product).
+struct Bf16Plan {
+    int64_t tiles = 0, dp = 0, sk = 0;
+    int parts = 1;
+    size_t workspace_bytes() const { return sk ? static_cast<size_t>(sk * parts) * kPartialVec * sizeof(f32x4) : 0; }
+};
+
+Bf16Plan bf16_plan(int64_t tiles, int64_t stages, int cus) {
+    Bf16Plan p;
+    p.tiles = p.dp = tiles;
+    if (cus <= 0 || tiles <= cus || tiles % cus == 0 || stages < 2) return p;
+    const int64_t sk = tiles % cus;
+    double best = 1.0;  // an unsplit last round: one tile's time
+    int best_parts = 1;
+    for (int parts = 2; parts <= 8 && parts <= stages; ++parts) {
+        const double rounds = static_cast<double>((sk * parts + cus - 1) / cus);
+        const double cost = rounds / parts + 0.09 * static_cast<double>(sk * parts) / cus;
+        if (cost < best - 1e-9) {
+            best = cost;
+            best_parts = parts;
+        }
+    }
+    if (best_parts == 1) return p;
+    p.dp = tiles - sk;
+    p.sk = sk;
+    p.parts = best_parts;
+    return p;
+}
+
+int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+bool bf16_symmetric(const float* C, const void* A, const void* B, int64_t M, int64_t N, int64_t lda, int64_t ldb,
+                    int64_t ldc) {
+    return A == B && lda == ldb && M == N && ldc % 4 == 0 && reinterpret_cast<uintptr_t>(C) % 16 == 0;
+}
+
+int64_t bf16_tiles(bool sym, int64_t M, int64_t N) {
+    const int64_t tm = (M + kT16 - 1) / kT16, tn = (N + kT16 - 1) / kT16;
+    return sym ? tm * (tm + 1) / 2 : tm * tn;
+}
+
 }  // namespace
 
 extern "C" {
 
-int qsrt_gemm_tn(float* C, const void* A, const void* B, const void* B2, int64_t M, int64_t N, int64_t K,
-                 int64_t lda, int64_t ldb, int64_t ldc, float alpha, int dtype, void* stream_handle) {
+size_t qsrt_gemm_tn_workspace_bytes(const float* C, const void* A, const void* B, int64_t M, int64_t N, int64_t K,
+                                    int64_t lda, int64_t ldb, int64_t ldc, int dtype) {
+    if (dtype != 1 || M <= 0 || N <= 0 || K <= 0) return 0;
+    const bool sym = bf16_symmetric(C, A, B, M, N, lda, ldb, ldc);
+    return bf16_plan(bf16_tiles(sym, M, N), (K + kBK16 - 1) / kBK16, device_cus()).workspace_bytes();
+}
+
+int qsrt_gemm_tn_ws(float* C, const void* A, const void* B, const void* B2, int64_t M, int64_t N, int64_t K,
+                    int64_t lda, int64_t ldb, int64_t ldc, float alpha, int dtype, void* workspace,
+                    size_t workspace_bytes, void* stream_handle) {
     hipStream_t stream = static_cast<hipStream_t>(stream_handle);
     if (dtype != 0 && dtype != 1) return qsrt::fail(qsrt::kBadArgument, "dtype must be 0 (f32) or 1 (bf16)");
     if (M < 0 || N < 0 || K < 0) return qsrt::fail(qsrt::kBadArgument, "negative GEMM extent");
@@ -360,37 +539,62 @@ int qsrt_gemm_tn(float* C, const void* A, const void* B, const void* B2, int64_t
     if (!C || !A || !B) return qsrt::fail(qsrt::kBadArgument, "null pointer argument");
     if (lda < M || ldb < N || ldc < N)
         return qsrt::fail(qsrt::kBadArgument, "leading dimensions must cover the rows (lda >= M, ldb >= N, ldc >= N)");
-    const int64_t tiles_n = (N + kBN - 1) / kBN;
-    const int64_t tiles = ((M + kBM - 1) / kBM) * tiles_n;
-    if (tiles > 0x7fffffff) return qsrt::fail(qsrt::kBadArgument, "GEMM too large for one launch");
     if (dtype == 0) {
+        const int64_t tiles_n = (N + kBN - 1) / kBN;
+        const int64_t tiles = ((M + kBM - 1) / kBM) * tiles_n;
+        if (tiles > 0x7fffffff) return qsrt::fail(qsrt::kBadArgument, "GEMM too large for one launch");
         if (lda % 4 || ldb % 4 || reinterpret_cast<uintptr_t>(A) % 16 || reinterpret_cast<uintptr_t>(B) % 16 ||
             (B2 && reinterpret_cast<uintptr_t>(B2) % 16))
             return qsrt::fail(qsrt::kBadArgument, "f32 operands must be 16-byte aligned with lda, ldb multiples of 4");
         hipLaunchKernelGGL(gemm_tn_f32_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, stream, C,
                            static_cast<const float*>(A), static_cast<const float*>(B), static_cast<const float*>(B2),
                            M, N, K, lda, ldb, ldc, alpha, tiles_n);
-    } else {
-        if (B2) return qsrt::fail(qsrt::kBadArgument, "the bf16 path has no fused subtraction");
-        if (lda % 8 || ldb % 8 || reinterpret_cast<uintptr_t>(A) % 16 || reinterpret_cast<uintptr_t>(B) % 16)
-            return qsrt::fail(qsrt::kBadArgument, "bf16 operands must be 16-byte aligned with lda, ldb multiples of 8");
-        if (lda > (1 << 23) || ldb > (1 << 23))
-            return qsrt::fail(qsrt::kBadArgument, "bf16 leading dimensions above 2^23 are not supported");
-        const int64_t tm = (M + kT16 - 1) / kT16, tn = (N + kT16 - 1) / kT16;
-        const bool sym = A == B && lda == ldb && M == N && ldc % 4 == 0 && reinterpret_cast<uintptr_t>(C) % 16 == 0;
-        const int64_t n = sym ? tm * (tm + 1) / 2 : tm * tn;
-        if (n > 0x7fffffff || tn > 0x7fffffff) return qsrt::fail(qsrt::kBadArgument, "GEMM too large for one launch");
-        if (sym)
-            hipLaunchKernelGGL(gemm_tn_bf16_kernel<true>, dim3(static_cast<unsigned>(n)), dim3(kThreads16), 0, stream,
-                               C, static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(B), M, N, K, lda, ldb,
-                               ldc, alpha, static_cast<int>(tn));
-        else
-            hipLaunchKernelGGL(gemm_tn_bf16_kernel<false>, dim3(static_cast<unsigned>(n)), dim3(kThreads16), 0,
-                               stream, C, static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(B), M, N, K,
-                               lda, ldb, ldc, alpha, static_cast<int>(tn));
+        QSRT_HIP_TRY(hipGetLastError());
+        return qsrt::kOk;
     }
+    if (B2) return qsrt::fail(qsrt::kBadArgument, "the bf16 path has no fused subtraction");
+    if (lda % 8 || ldb % 8 || reinterpret_cast<uintptr_t>(A) % 16 || reinterpret_cast<uintptr_t>(B) % 16)
+        return qsrt::fail(qsrt::kBadArgument, "bf16 operands must be 16-byte aligned with lda, ldb multiples of 8");
+    if (lda > (1 << 23) || ldb > (1 << 23))
+        return qsrt::fail(qsrt::kBadArgument, "bf16 leading dimensions above 2^23 are not supported");
+    const int64_t tn = (N + kT16 - 1) / kT16;
+    const bool sym = bf16_symmetric(C, A, B, M, N, lda, ldb, ldc);
+    const int64_t tiles = bf16_tiles(sym, M, N);
+    if (tiles > 0x7fffffff / 8 || tn > 0x7fffffff) return qsrt::fail(qsrt::kBadArgument, "GEMM too large for one launch");
+    Bf16Plan plan = bf16_plan(tiles, (K + kBK16 - 1) / kBK16, device_cus());
+    if (plan.sk && (!workspace || workspace_bytes < plan.workspace_bytes() ||
+                    reinterpret_cast<uintptr_t>(workspace) % 16)) {
+        plan.dp = tiles;  // no room for the split tiles' partials: every tile whole, as qsrt_gemm_tn runs them
+        plan.sk = 0;
+        plan.parts = 1;
+    }
+    const unsigned grid = static_cast<unsigned>(plan.dp + plan.sk * plan.parts);
+    auto* ws = static_cast<f32x4*>(workspace);
+    const auto* a = static_cast<const uint16_t*>(A);
+    const auto* b = static_cast<const uint16_t*>(B);
+    const int dp = static_cast<int>(plan.dp), sk = static_cast<int>(plan.sk), ti = static_cast<int>(tn);
+    if (sym)
+        hipLaunchKernelGGL(gemm_tn_bf16_kernel<true>, dim3(grid), dim3(kThreads16), 0, stream, C, a, b, M, N, K, lda,
+                           ldb, ldc, alpha, ti, dp, sk, plan.parts, ws);
+    else
+        hipLaunchKernelGGL(gemm_tn_bf16_kernel<false>, dim3(grid), dim3(kThreads16), 0, stream, C, a, b, M, N, K, lda,
+                           ldb, ldc, alpha, ti, dp, sk, plan.parts, ws);
     QSRT_HIP_TRY(hipGetLastError());
+    if (plan.sk) {
+        if (sym)
+            hipLaunchKernelGGL(gemm_tn_bf16_fixup<true>, dim3(static_cast<unsigned>(sk) * 8u), dim3(kThreads16), 0, stream,
+                               C, M, N, ldc, alpha, ti, dp, sk, plan.parts, ws);
+        else
+            hipLaunchKernelGGL(gemm_tn_bf16_fixup<false>, dim3(static_cast<unsigned>(sk) * 8u), dim3(kThreads16), 0, stream,
+                               C, M, N, ldc, alpha, ti, dp, sk, plan.parts, ws);
+        QSRT_HIP_TRY(hipGetLastError());
+    }
     return qsrt::kOk;
+}
+
+int qsrt_gemm_tn(float* C, const void* A, const void* B, const void* B2, int64_t M, int64_t N, int64_t K,
+                 int64_t lda, int64_t ldb, int64_t ldc, float alpha, int dtype, void* stream_handle) {
+    return qsrt_gemm_tn_ws(C, A, B, B2, M, N, K, lda, ldb, ldc, alpha, dtype, nullptr, 0, stream_handle);
 }
 
 }  // extern "C"

@@ -22,10 +22,16 @@ def _launch(C, A, B, B2, alpha, dtype):
     K, M = A.shape
     N = B.shape[1]
     lib = _native.lib()
+    args = (C.data_ptr(), A.data_ptr(), B.data_ptr())
+    lds = (A.stride(0), B.stride(0), C.stride(0))
+    # the split tiles' partial products (bf16 tile counts that leave the last round of CUs part-empty) go to a
+    # workspace from torch's stream-ordered allocator
+    nbytes = lib.qsrt_gemm_tn_workspace_bytes(*args, M, N, K, *lds, dtype)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=C.device) if nbytes else None
     _native.check(
-        lib.qsrt_gemm_tn(C.data_ptr(), A.data_ptr(), B.data_ptr(), None if B2 is None else B2.data_ptr(), M, N, K,
-                         A.stride(0), B.stride(0), C.stride(0), float(alpha), dtype, _native.stream_handle(C.device)),
-        "qsrt_gemm_tn",
+        lib.qsrt_gemm_tn_ws(*args, None if B2 is None else B2.data_ptr(), M, N, K, *lds, float(alpha), dtype,
+                            None if ws is None else ws.data_ptr(), nbytes, _native.stream_handle(C.device)),
+        "qsrt_gemm_tn_ws",
     )
 
 

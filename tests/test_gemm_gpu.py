@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from qsrt_amd import gemm
+from qsrt_amd import _native, gemm
 
 pytestmark = pytest.mark.gpu
 
@@ -115,6 +115,64 @@ def test_bf16_general_product_matches_float64(K, M, N):
     gemm._launch(C, gemm._aligned(A.cuda(), 8), gemm._aligned(B.cuda(), 8), None, 0.25, 1)
     want = C0.double().numpy() + 0.25 * (A.double().numpy().T @ B.double().numpy())
     assert _rel(C.cpu().double().numpy(), want) < 1e-5
+
+
+def _bf16_call(C, A, B, alpha, workspace=None, nbytes=None):
+    """qsrt_gemm_tn_ws with an explicit workspace (None: qsrt_gemm_tn)."""
+
+    lib = _native.lib()
+    K, M = A.shape
+    N = B.shape[1]
+    stream = _native.stream_handle(C.device)
+    if workspace is None:
+        rc = lib.qsrt_gemm_tn(C.data_ptr(), A.data_ptr(), B.data_ptr(), None, M, N, K, A.stride(0), B.stride(0),
+                              C.stride(0), float(alpha), 1, stream)
+    else:
+        rc = lib.qsrt_gemm_tn_ws(C.data_ptr(), A.data_ptr(), B.data_ptr(), None, M, N, K, A.stride(0), B.stride(0),
+                                 C.stride(0), float(alpha), 1, workspace.data_ptr(),
+                                 workspace.numel() if nbytes is None else nbytes, stream)
+    assert rc == 0, lib.qsrt_last_error().decode()
+
+
+@pytest.mark.parametrize("K,M,N,sym", [(640, 5888, 5888, True), (1000, 4504, 4504, False), (640, 4352, 4600, False),
+                                       (16384, 7168, 7168, False)])
+def test_bf16_split_last_round(K, M, N, sym):
+    """Tile counts that leave the last round of CUs part-empty split that
+    round's tiles along K (partials in the workspace, added in K order by the
+    fixup kernel): the result matches float64 and the unsplit kernel to FP32
+    rounding, is identical from call to call, and a short workspace runs the
+    unsplit kernel bit for bit."""
+
+    print(f"[gemm] bf16 split K{K} M{M} N{N} sym={sym}", file=sys.stderr, flush=True)
+    g = torch.Generator(device="cuda").manual_seed(K + M + N)
+    A = torch.randn(K, M, device="cuda", generator=g).bfloat16()
+    B = A if sym else torch.randn(K, N, device="cuda", generator=g).bfloat16()
+    C0 = torch.randn(M, N, device="cuda", generator=g)
+    if sym:
+        C0 = C0 + C0.T
+    lib = _native.lib()
+    nbytes = lib.qsrt_gemm_tn_workspace_bytes(C0.data_ptr(), A.data_ptr(), B.data_ptr(), M, N, K, A.stride(0),
+                                              B.stride(0), C0.stride(0), 1)
+    assert nbytes > 0 and nbytes % (256 * 1024) == 0  # split tiles x parts partials of 256 KiB
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    split = C0.clone()
+    _bf16_call(split, A, B, 0.5, ws)
+    again = C0.clone()
+    _bf16_call(again, A, B, 0.5, ws)
+    whole = C0.clone()
+    _bf16_call(whole, A, B, 0.5)
+    short = C0.clone()
+    _bf16_call(short, A, B, 0.5, ws, nbytes - 16)
+    torch.cuda.synchronize()
+    assert torch.equal(split, again)
+    assert torch.equal(short, whole)
+    ref = C0.double() + 0.5 * (A.double().T @ B.double())
+    scale = ref.abs().max().item()
+    assert (split.double() - ref).abs().max().item() / scale < 1e-5
+    assert (split - whole).abs().max().item() / scale < 1e-5
+    if sym:
+        assert torch.equal(split, split.T)
+    assert not torch.equal(split, whole) or K < 128  # the split tiles did take the partial path
 
 
 def test_gemm_rejects_bad_arguments():
