@@ -63,8 +63,9 @@ VITERBI_HBM_BYTES_PER_TILE = {2: 1.631e6, 3: 1.633e6, 4: 0.816e6}
 # Same counters for the decode launches: 1.013 x their algorithmic bytes (profiles/decode_kernel_layer.md).
 DECODE_TRAFFIC_OVER_ALGORITHMIC = 1.013
 # Same counters at the bench's GEMM and Hadamard shapes (profiles/gemm_tn_kernels_expert_shapes.md,
-# profiles/hadamard_kernel_expert_matrix.md): HBM bytes per launch.
-GEMM_HBM_BYTES = {"hessian_capture": 2.415e9, "ldlq_span_update": 1.485e8}
+# profiles/hadamard_kernel_expert_matrix.md): HBM bytes per launch (the Hessian capture: its main kernel and
+# the fixup kernel of its K-split tiles together).
+GEMM_HBM_BYTES = {"hessian_capture": 2.435e9, "ldlq_span_update": 1.485e8}
 HADAMARD_HBM_BYTES = {"left": 1.1782e8, "right": 1.1765e8}
 
 LAYER_EXPERTS = 384
