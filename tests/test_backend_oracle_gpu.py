@@ -124,6 +124,48 @@ def test_regularize_on_device_matches_oracle_at_fixed_scale():
     be._SHARED_INPUT_SCALES.pop(key, None)
 
 
+@pytest.mark.parametrize("apply_out", [False, True])
+def test_regularize_fused_division_equals_two_step(apply_out):
+    """The device regularize divides by sv and su inside the rotation kernel
+    (its pre-divisor).  That must be the separate correctly rounded divide
+    followed by the rotation, bit for bit, dead channels included."""
+
+    from qsrt_amd import hadamard
+
+    k, n = 512, 768
+    gen = torch.Generator().manual_seed(72)
+    W = bench.student_t_like((k, n), std=0.02, gen=gen)
+    W[:, 5] = 0.0  # a dead output channel
+    W[7, :] = 0.0
+    su = torch.from_numpy(_signs(k, 8)).float().reshape(-1, 1).to(DEV)
+    sv = torch.from_numpy(_signs(n, 9)).float().reshape(1, -1).to(DEV)
+    qa = {"apply_out_scales": apply_out, "g_scale_override": 0.9}
+    _, W_r, g, su_r, sv_r = be.regularize(W.to(DEV).clone(), su.clone(), sv.clone(), qa, False, None, None)
+    # the same steps as separate kernels
+    w = W.to(DEV).clone()
+    scales = be.block_rms(w, dim=0, keepdim=True)
+    scales /= scales.mean().item()  # a host scalar, as regularize divides (torch multiplies by its reciprocal)
+    dead = scales.abs() < 1e-30
+    sv2 = sv.clone()
+    if apply_out:
+        scales[dead] = 0.1
+        sv2 = (sv2 * scales + 1e-10).float()
+    w /= sv2
+    sv2[dead] = 0.0
+    hadamard.rotate_(w, 128, side="right")
+    rows = be.block_rms(w, dim=1, keepdim=True)
+    rows[rows.abs() < 1e-30] = 0.1
+    su2 = (su * rows / (-be.codebook_scale) + 1e-10).float()
+    w /= su2
+    hadamard.rotate_(w, 128, side="left")
+    w *= g
+    su2 /= g
+    torch.cuda.synchronize()
+    assert torch.equal(W_r, w)
+    assert torch.equal(su_r, su2)
+    assert torch.equal(sv_r, sv2)
+
+
 def _problem(k: int, n: int, seed: int):
     H_sum = _hessian_sum(k, 4 * k, 0.8, seed)
     Hp = oenc.prepare_hessian(H_sum.double().numpy(), 4 * k, 0.01)
