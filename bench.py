@@ -562,7 +562,7 @@ def layer_cpu_sample(first: dict, source: dict, blocks: int = 96) -> dict:
     t0 = time.perf_counter()
     rec = oenc.blockldlq(W_gpu, L_gpu, tile_bits, labels, lags, threads=threads)
     t_rec = time.perf_counter() - t0
-    rec_stats = oenc.compare_states(gpu_states, rec, labels, tile_bits)
+    rec_stats = oenc.compare_states(gpu_states, rec, labels, tile_bits, lags)
 
     spec = CoupledHadamardSpec()
     w = tuple(t.float() for t in source["w"])
@@ -579,13 +579,15 @@ def layer_cpu_sample(first: dict, source: dict, blocks: int = 96) -> dict:
     H_c, L0 = oenc.factor(H, su)
     t_prep = time.perf_counter() - t0
     e2e = oenc.blockldlq(W_r[-rows:], L0[-rows:, -rows:], tile_bits, labels, lags, threads=threads)
-    e2e_stats = oenc.compare_states(gpu_states, e2e, labels, tile_bits)
+    e2e_stats = oenc.compare_states(gpu_states, e2e, labels, tile_bits, lags)
     n_w = rows * LAYER_INTER
 
     def parity(stats, what):
         return {"what": what, "tiles": stats["tiles"], "tiles_differing": stats["differ"],
                 "mismatch_rate": stats["mismatch_rate"], "near_tie_tiles": len(stats["first"]),
-                "max_near_tie_sse_rel": float(max(stats["sse_rel_deltas"], default=0.0))}
+                "max_near_tie_sse_rel": float(max(stats["sse_rel_deltas"], default=0.0)),
+                "boundary_ties": stats["kinds"].count("boundary"),
+                "max_boundary_margin": float(max(stats["boundary_margins"], default=0.0))}
 
     return {
         "cpu": {"value": round(n_w / t_rec / 1e6, 5), "unit": "M weights/s", "cores": threads, "kind": "port",

@@ -138,7 +138,8 @@ def tile_sse(labels_tiles: np.ndarray, targets: np.ndarray) -> np.ndarray:
     return np.sum(d * d, axis=-1)
 
 
-def compare_states(gpu_states: np.ndarray, cpu: dict, labels: dict, tile_bits: np.ndarray) -> dict:
+def compare_states(gpu_states: np.ndarray, cpu: dict, labels: dict, tile_bits: np.ndarray, lags: dict, *,
+                   context: int = 128) -> dict:
     """Tile-level agreement of a GPU encode with ``cpu`` (a ``blockldlq``
     result on the same inputs).
 
@@ -147,14 +148,30 @@ def compare_states(gpu_states: np.ndarray, cpu: dict, labels: dict, tile_bits: n
     differs while every tile below it in its column agrees saw the same target
     up to rounding: that is a resolution of a near-tie (``first``).  Tiles
     above a differing tile in the same column saw different targets
-    (``propagated``).  For every ``first`` tile the relative SSE delta of the
-    two paths on the CPU target is returned."""
+    (``propagated``).
+
+    A ``first`` tile is one of two kinds, told apart by the state before
+    position 0 (``codeword[0] >> K``, the tile's end_state):
+
+    * ``path``: both encodes chose the same end_state, so both paths are
+      closed paths through it and the constrained pass resolved a tie; the
+      delta is the relative SSE of the two paths on the CPU target;
+    * ``boundary``: the end_states differ, i.e. the primer's choice resolved a
+      tie (between two read costs, or between two primer paths into the
+      chosen state that pass through different boundary states).  The delta
+      is the GPU path's relative SSE against the best closed path through the
+      GPU's own end_state, and the margin says how close the primer came to
+      choosing that end_state: the least, over states ``s``, of the larger of
+      ``s``'s read cost above the minimum and the cost of the best primer
+      path into ``s`` through the GPU's end_state above ``s``'s final cost,
+      both relative (0 for a ``path`` tile; ``inf`` if no primer path
+      reaches it).  Both are on the CPU target."""
 
     g = np.asarray(gpu_states, dtype=np.uint16)
     c = cpu["states"]
     kt, nt, _ = c.shape
     differ = np.any(g != c, axis=2)
-    first, propagated, deltas = [], [], []
+    first, kinds, propagated, deltas, margins = [], [], [], [], []
     for col in range(nt):
         seen = False
         for rb in range(kt - 1, -1, -1):  # the recursion's order: bottom block first
@@ -168,15 +185,33 @@ def compare_states(gpu_states: np.ndarray, cpu: dict, labels: dict, tile_bits: n
             bits = int(tile_bits[rb, col])
             lab = labels[bits]
             t = cpu["targets"][rb, col]
-            sse_c = tile_sse(lab[c[rb, col].astype(np.int64)], t)
             sse_g = tile_sse(lab[g[rb, col].astype(np.int64)], t)
-            deltas.append(abs(sse_g - sse_c) / max(sse_c, 1e-30))
+            end_g, end_c = int(g[rb, col, 0]) >> bits, int(c[rb, col, 0]) >> bits
+            if end_g == end_c:
+                kinds.append("path")
+                sse_c = tile_sse(lab[c[rb, col].astype(np.int64)], t)
+                deltas.append(abs(sse_g - sse_c) / max(sse_c, 1e-30))
+                margins.append(0.0)
+                continue
+            kinds.append("boundary")
+            _, best = ov.encode_from(t[None], lab, [end_g], K=bits, threads=1)
+            sse_b = tile_sse(lab[best[0].astype(np.int64)], t)
+            deltas.append(abs(sse_g - sse_b) / max(sse_b, 1e-30))
+            cost, final, _ = ov.boundary_view(t, lab, K=bits, context=context, boundary_lag=lags[bits])
+            through = ov.primer_through(t, lab, end_g, K=bits, context=context).astype(np.float64)
+            read_gap = (cost.astype(np.float64) - float(cost.min())) / max(float(cost.min()), 1e-30)
+            with np.errstate(invalid="ignore"):
+                path_gap = (through - final) / np.maximum(final.astype(np.float64), 1e-30)
+            margin = np.maximum(read_gap, path_gap)
+            margins.append(float(np.nanmin(margin)) if np.isfinite(margin).any() else float("inf"))
     return {
         "tiles": int(kt * nt),
         "differ": int(differ.sum()),
         "first": first,
+        "kinds": kinds,
         "propagated": len(propagated),
         "sse_rel_deltas": deltas,
+        "boundary_margins": margins,
         "mismatch_rate": float(differ.sum()) / float(kt * nt),
         "states_differing": int(np.sum(g != c)),
     }

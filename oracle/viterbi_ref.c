@@ -120,9 +120,11 @@ static void vt_step16(const float *lab, const float *prev, float *next, uint8_t 
 #endif
 
 /* One forward pass; returns the buffer holding the final costs and, via
- * *penult, the buffer holding the costs one step earlier. */
+ * *penult, the buffer holding the costs one step earlier.  pre_state < 0
+ * starts free (every state at cost 0); otherwise the first step admits only
+ * predecessor pre_state, carrying cost pre_cost. */
 static float *vt_forward(vt_ctx *c, const float *lab, const float *x, int roll, int steps,
-                         int pre_state, int trace_start, float **penult)
+                         int pre_state, float pre_cost, int trace_start, float **penult)
 {
     const int S = c->S, P = c->P, K = c->K, L = c->L;
     const int pred_shift = L - 2 * K, word_shift = L - K;
@@ -151,7 +153,7 @@ static float *vt_forward(vt_ctx *c, const float *lab, const float *x, int roll, 
                 float cost;
                 if (i == 0) {
                     const int pred = (k << pred_shift) | q;
-                    cost = (pre_state < 0 || pred == pre_state) ? fmaf(d, d, 0.0f) : INFINITY;
+                    cost = pre_state < 0 ? fmaf(d, d, 0.0f) : pred == pre_state ? fmaf(d, d, pre_cost) : INFINITY;
                 } else {
                     cost = fmaf(d, d, prev[(k << pred_shift) | q]);
                 }
@@ -199,6 +201,22 @@ static int vt_trace(const vt_ctx *c, int roll, int steps, int edge, const float 
     return edge;
 }
 
+static int vt_ctx_init(vt_ctx *c, int L, int K, int T)
+{
+    c->L = L; c->K = K; c->T = T; c->S = 1 << (L - K); c->P = 1 << K;
+    c->a = (float *)malloc(sizeof(float) * c->S);
+    c->b = (float *)malloc(sizeof(float) * c->S);
+    c->dec = (uint8_t *)calloc((size_t)T * c->S, 1);
+    return c->a && c->b && c->dec;
+}
+
+static void vt_ctx_free(vt_ctx *c)
+{
+    free(c->a);
+    free(c->b);
+    free(c->dec);
+}
+
 /*
  * tiles, recon: [n_tiles, T] float; states: [n_tiles, T] uint16;
  * labels: [2^L] float, state(codeword)-indexed; boundary (optional):
@@ -221,26 +239,117 @@ int qsrt_oracle_viterbi(const float *tiles, float *recon, uint16_t *states, int6
 #pragma omp parallel reduction(| : failed)
     {
         vt_ctx c;
-        c.L = L; c.K = K; c.T = T; c.S = 1 << (L - K); c.P = 1 << K;
-        c.a = (float *)malloc(sizeof(float) * c.S);
-        c.b = (float *)malloc(sizeof(float) * c.S);
-        c.dec = (uint8_t *)calloc((size_t)T * c.S, 1);
-        if (!c.a || !c.b || !c.dec) failed = 1;
+        if (!vt_ctx_init(&c, L, K, T)) failed = 1;
 #pragma omp for schedule(dynamic, 1)
         for (int64_t t = 0; t < n_tiles; ++t) {
             if (failed) continue;
             const float *x = tiles + t * T;
             float *penult;
-            float *fin = vt_forward(&c, labels, x, T - C, 2 * C, -1, C, &penult);
+            float *fin = vt_forward(&c, labels, x, T - C, 2 * C, -1, 0.0f, C, &penult);
             const int start = vt_argmin(boundary_lag ? penult : fin, c.S);
             const int end_state = vt_trace(&c, T - C, 2 * C, start, labels, NULL, NULL);
-            vt_forward(&c, labels, x, 0, T, end_state, 0, &penult);
+            vt_forward(&c, labels, x, 0, T, end_state, 0.0f, 0, &penult);
             vt_trace(&c, 0, T, end_state, labels, states + t * T, recon + t * T);
             if (boundary) boundary[t] = end_state;
         }
-        free(c.a);
-        free(c.b);
-        free(c.dec);
+        vt_ctx_free(&c);
+    }
+    return failed ? -2 : 0;
+}
+
+/*
+ * The boundary choice of one tile (steps 1-3 above) laid open: cost [S]
+ * receives the primer costs that the boundary argmin reads (the final ones,
+ * or those one step earlier when boundary_lag = 1), final [S] (optional) the
+ * final primer costs, and end_of [S] the end_state that each state's primer
+ * survivor traces back to.  Returns 0, -1 on bad arguments, -2 on allocation
+ * failure.
+ */
+int qsrt_oracle_viterbi_boundary(const float *tile, int L, int K, int T, int C, const float *labels,
+                                 int boundary_lag, float *cost, float *final, int32_t *end_of)
+{
+    if (L < 2 || L > 16 || K < 1 || 2 * K > L || T < 2 || C < 1 || 2 * C > T ||
+        (boundary_lag != 0 && boundary_lag != 1))
+        return -1;
+    vt_ctx c;
+    int rc = 0;
+    if (vt_ctx_init(&c, L, K, T)) {
+        float *penult;
+        const float *fin = vt_forward(&c, labels, tile, T - C, 2 * C, -1, 0.0f, C, &penult);
+        memcpy(cost, boundary_lag ? penult : fin, sizeof(float) * c.S);
+        if (final) memcpy(final, fin, sizeof(float) * c.S);
+        for (int s = 0; s < c.S; ++s)
+            end_of[s] = vt_trace(&c, T - C, 2 * C, s, labels, NULL, NULL);
+    } else {
+        rc = -2;
+    }
+    vt_ctx_free(&c);
+    return rc;
+}
+
+/*
+ * The primer restricted to paths whose state before position 0 is e:
+ * through [S] receives, per final state, the cost of the best primer path
+ * through e, computed with the primer's own operations in the primer's
+ * order, so through[s] == final[s] exactly when state s's primer survivor
+ * passes through e (ties included) and through[s] > final[s] otherwise.
+ * Two encodes of nearly equal targets pick different end_states when, for
+ * the state the boundary argmin picks, a path through another boundary
+ * state costs nearly the same; this measures that margin.  Returns 0, -1 on
+ * bad arguments, -2 on allocation failure.
+ */
+int qsrt_oracle_viterbi_primer_through(const float *tile, int L, int K, int T, int C, const float *labels,
+                                       int e, float *through)
+{
+    if (L < 2 || L > 16 || K < 1 || 2 * K > L || T < 2 || C < 1 || 2 * C > T || e < 0 || e >= (1 << (L - K)))
+        return -1;
+    vt_ctx c;
+    int rc = 0;
+    if (vt_ctx_init(&c, L, K, T)) {
+        float *penult;
+        const float *head = vt_forward(&c, labels, tile, T - C, C, -1, 0.0f, C, &penult);
+        const float at_e = head[e];
+        const float *fin = vt_forward(&c, labels, tile, 0, C, e, at_e, C, &penult);
+        memcpy(through, fin, sizeof(float) * c.S);
+    } else {
+        rc = -2;
+    }
+    vt_ctx_free(&c);
+    return rc;
+}
+
+/*
+ * Steps 4-5 alone: the constrained pass and trace of each tile from a given
+ * end_state (end_states [n_tiles], each < 2^(L-K)), i.e. the best tail-biting
+ * path through that boundary state.  Returns 0, -1 on bad arguments, -2 on
+ * allocation failure.
+ */
+int qsrt_oracle_viterbi_from(const float *tiles, float *recon, uint16_t *states, int64_t n_tiles,
+                             int L, int K, int T, const float *labels, const int32_t *end_states,
+                             int n_threads)
+{
+    if (L < 2 || L > 16 || K < 1 || 2 * K > L || T < 2 || n_tiles < 0)
+        return -1;
+    for (int64_t t = 0; t < n_tiles; ++t)
+        if (end_states[t] < 0 || end_states[t] >= (1 << (L - K))) return -1;
+    int failed = 0;
+#ifdef _OPENMP
+    if (n_threads > 0) omp_set_num_threads(n_threads);
+#else
+    (void)n_threads;
+#endif
+#pragma omp parallel reduction(| : failed)
+    {
+        vt_ctx c;
+        if (!vt_ctx_init(&c, L, K, T)) failed = 1;
+#pragma omp for schedule(dynamic, 1)
+        for (int64_t t = 0; t < n_tiles; ++t) {
+            if (failed) continue;
+            float *penult;
+            vt_forward(&c, labels, tiles + t * T, 0, T, end_states[t], 0.0f, 0, &penult);
+            vt_trace(&c, 0, T, end_states[t], labels, states + t * T, recon + t * T);
+        }
+        vt_ctx_free(&c);
     }
     return failed ? -2 : 0;
 }

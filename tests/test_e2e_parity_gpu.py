@@ -12,12 +12,20 @@ recursion.
 Bars: packed words equal byte for byte wherever the
 paths agree; a tile whose path differs while every tile below it in its
 column agrees saw the same target up to FP32 rounding, so it is a near-tie
-resolved the other way, and its squared error must be within 1e-6 relative
-of the CPU path's on the CPU target.  The tile mismatch rate is printed.
-Tiles above such a tile in the same column see a different target (the
-feedback runs along columns), so they are counted but not held to the tie
-bar; their effect is bounded through the proxy error, and the near-tie
-events themselves must stay rare (at most one per 256 tiles, or one).
+resolved the other way.  When both paths pass through the same boundary
+state (the state before position 0) the tie was in the constrained pass,
+and the GPU path's squared error must be within 1e-6 relative of the CPU
+path's on the CPU target.  When the boundary states differ the tie was in
+the primer's boundary choice: the primer must have come within 1e-6
+relative of choosing the GPU's boundary state, and the GPU path must then
+be the best closed path through it (squared error within 1e-6 relative).
+The two end in paths whose errors may differ by far more than 1e-6, which is
+the reference's boundary rule at work, not a kernel error.  The tile
+mismatch rate is printed.  Tiles above such a tile in the same column see a
+different target (the feedback runs along columns), so they are counted but
+not held to the tie bar; their effect is bounded through the proxy error,
+and the near-tie events themselves must stay rare (at most one per 256
+tiles, or one).
 """
 
 from __future__ import annotations
@@ -66,13 +74,24 @@ def _gpu_encode(W: torch.Tensor, H_sum: torch.Tensor, count: int, bits: int, see
 
 
 def _check_tie_events(name: str, stats: dict) -> None:
-    """Near-tie events stay rare.  Each one is held to the SSE bar above;
-    the tiles above it in its column then see other targets and may differ
-    too (they are counted in the mismatch rate, and bounded through the
-    proxy error), so the bound is on events, not on differing tiles."""
+    """Each near-tie event meets the bar of its kind, and the events stay
+    rare.  The tiles above an event in its column then see other targets and
+    may differ too (they are counted in the mismatch rate, and bounded
+    through the proxy error), so the bound is on events, not on differing
+    tiles."""
 
+    for (rb, col), kind, d, m in zip(stats["first"], stats["kinds"], stats["sse_rel_deltas"],
+                                     stats["boundary_margins"]):
+        assert m <= TIE_SSE_REL, f"{name}: tile ({rb}, {col}) boundary state is {m:.3e} relative from a tie"
+        assert d <= TIE_SSE_REL, f"{name}: tile ({rb}, {col}) ({kind}) SSE is {d:.3e} relative from the CPU path's"
     events = len(stats["first"])
     assert events <= max(1, stats["tiles"] // 256), f"{name}: {events} near-tie events in {stats['tiles']} tiles"
+
+
+def _tie_summary(stats: dict) -> str:
+    d, m = stats["sse_rel_deltas"], stats["boundary_margins"]
+    return (f"{stats['kinds'].count('path')} path and {stats['kinds'].count('boundary')} boundary near-ties, "
+            f"max SSE delta {max(d, default=0.0):.3e}, max boundary margin {max(m, default=0.0):.3e}")
 
 
 def _check_matrix(name: str, W: torch.Tensor, H_sum: torch.Tensor, count: int, bits: int, seeds) -> dict:
@@ -87,14 +106,13 @@ def _check_matrix(name: str, W: torch.Tensor, H_sum: torch.Tensor, count: int, b
     cpu = oenc.encode_matrix(W.double().cpu().numpy(), H_sum.double().cpu().numpy(), count,
                              _signs(k, seeds.input_sign), _signs(n, seeds.output_sign), qa["g_scale"],
                              np.full((k // 16, n // 16), bits), labels, lags, sigma_reg=0.01)
-    stats = oenc.compare_states(g_states, cpu, labels, np.full((k // 16, n // 16), bits))
+    stats = oenc.compare_states(g_states, cpu, labels, np.full((k // 16, n // 16), bits), lags)
     words = ofmt.pack_words(cpu["states"], bits)
     same_tile = ~np.any(g_states != cpu["states"], axis=2)
     cpu_proxy = oenc.proxy(cpu["W_r"], cpu["Q"], cpu["H_c"])
-    deltas = stats["sse_rel_deltas"]
     _say(f"[e2e] {name}: {stats['differ']} of {stats['tiles']} tiles differ (mismatch rate "
-         f"{stats['mismatch_rate']:.5f}; {len(stats['first'])} near-tie, {stats['propagated']} downstream), "
-         f"max near-tie SSE delta {max(deltas) if deltas else 0.0:.3e}; proxy GPU {proxy:.6f} CPU {cpu_proxy:.6f}")
+         f"{stats['mismatch_rate']:.5f}; {stats['propagated']} downstream of {_tie_summary(stats)}); "
+         f"proxy GPU {proxy:.6f} CPU {cpu_proxy:.6f}")
     # words of every agreeing tile are the oracle's, byte for byte
     assert np.array_equal(trellis[same_tile], words[same_tile])
     # GPU's factor and conditioned metric against the float64 congruence + block LDL
@@ -107,8 +125,6 @@ def _check_matrix(name: str, W: torch.Tensor, H_sum: torch.Tensor, count: int, b
     # the GPU's reconstruction (regularised basis) is its states' labels
     assert np.array_equal(weight_q.cpu().numpy()[np.kron(same_tile, np.ones((16, 16), bool))],
                           cpu["Q"].astype(np.float32)[np.kron(same_tile, np.ones((16, 16), bool))])
-    for d in deltas:
-        assert d <= TIE_SSE_REL, f"{name}: a differing tile's SSE is {d:.3e} relative from the CPU path's"
     assert abs(proxy - cpu_proxy) <= 1e-3 * cpu_proxy
     _check_tie_events(name, stats)
     return stats
@@ -202,13 +218,9 @@ def test_batch_conditioned_path_matches_cpu_encode():
         cpu = oenc.encode_matrix(Wd, H_sum.double().numpy(), rows, su_s, sv_s, res[0]["g_scale"], tile_bits, labels,
                                  lags, sigma_reg=0.01, conditioned=True, g_into_sv=True, input_scales=profile)
         g_states = res[0]["encoded"].cpu().numpy().view(np.uint16)
-        stats = oenc.compare_states(g_states, cpu, labels, tile_bits)
-        deltas = stats["sse_rel_deltas"]
-        _say(f"[e2e] batch {matrix}: {stats['differ']} of {stats['tiles']} tiles differ, max near-tie SSE delta "
-             f"{max(deltas) if deltas else 0.0:.3e}; proxy GPU {res[0]['proxy']:.6f} CPU "
-             f"{oenc.proxy(cpu['W_r'], cpu['Q'], cpu['H_c']):.6f}")
-        for dlt in deltas:
-            assert dlt <= TIE_SSE_REL
+        stats = oenc.compare_states(g_states, cpu, labels, tile_bits, lags)
+        _say(f"[e2e] batch {matrix}: {stats['differ']} of {stats['tiles']} tiles differ, {_tie_summary(stats)}; "
+             f"proxy GPU {res[0]['proxy']:.6f} CPU {oenc.proxy(cpu['W_r'], cpu['Q'], cpu['H_c']):.6f}")
         cpu_proxy = oenc.proxy(cpu["W_r"], cpu["Q"], cpu["H_c"])
         assert abs(res[0]["proxy"] - cpu_proxy) <= 5e-3 * cpu_proxy
         _check_tie_events(f"batch {matrix}", stats)

@@ -101,12 +101,12 @@ def test_compare_states_classifies_planted_differences(small_encode):
     out, bits = small_encode
     kt, nt = bits.shape
     g = out["states"].copy()
-    assert oenc.compare_states(g, out, LABELS, bits)["differ"] == 0
+    assert oenc.compare_states(g, out, LABELS, bits, LAGS)["differ"] == 0
     # column 1: bottom block and one above it differ; column 4: only the top block
     g[kt - 1, 1, 7] ^= 1
     g[1, 1, 0] ^= 1
     g[0, 4, 3] ^= 1
-    stats = oenc.compare_states(g, out, LABELS, bits)
+    stats = oenc.compare_states(g, out, LABELS, bits, LAGS)
     assert stats["differ"] == 3
     assert sorted(stats["first"]) == sorted([(kt - 1, 1), (0, 4)])
     assert stats["propagated"] == 1
@@ -114,6 +114,35 @@ def test_compare_states_classifies_planted_differences(small_encode):
     assert len(stats["sse_rel_deltas"]) == 2 and all(d >= 0 for d in stats["sse_rel_deltas"])
     # a classification that walks the column top-down would name (1, 1) first
     assert (1, 1) not in stats["first"]
+    assert stats["kinds"] == ["path", "path"] and stats["boundary_margins"] == [0.0, 0.0]
+
+
+def test_compare_states_holds_a_planted_boundary_choice_to_its_margin(small_encode):
+    """A tile re-encoded through another boundary state is a ``boundary``
+    event: its path is the best one through that state (delta 0), but on
+    these inputs the primer is nowhere near choosing it (margin far above
+    any rounding); a path through that state that is not the best one shows
+    a positive delta."""
+
+    from oracle import viterbi as ov
+
+    out, bits = small_encode
+    kt, nt = bits.shape
+    rb, col = kt - 1, 3
+    b = int(bits[rb, col])
+    t = out["targets"][rb, col]
+    own = int(out["states"][rb, col, 0]) >> b
+    other = (own + 12345) % (1 << (16 - b))
+    _, via_other = ov.encode_from(t[None], LABELS[b], [other], K=b, threads=1)
+    g = out["states"].copy()
+    g[rb, col] = via_other[0]
+    stats = oenc.compare_states(g, out, LABELS, bits, LAGS)
+    assert stats["first"] == [(rb, col)] and stats["kinds"] == ["boundary"]
+    assert stats["sse_rel_deltas"] == [0.0]
+    assert stats["boundary_margins"][0] > 1e-3
+    g[rb, col, 100] ^= 1  # no longer the best path through `other`
+    stats = oenc.compare_states(g, out, LABELS, bits, LAGS)
+    assert stats["kinds"] == ["boundary"] and stats["sse_rel_deltas"][0] > 0.0
 
 
 @pytest.mark.parametrize("g_into_sv", (False, True))
@@ -145,3 +174,35 @@ def test_prepare_hessian_damps_the_mean_diagonal():
     H = oenc.prepare_hessian(H_sum, 7, 0.05)
     base = H_sum / 7
     assert np.allclose(H - base, 0.05 * np.mean(np.diag(base)) * np.eye(32))
+
+
+def test_observed_boundary_ties_are_ties():
+    """Tiles where an MI355X encode chose another boundary state than the
+    oracle on the same target (``tests/golden/boundary_ties_k3.npz``, written
+    by ``tests/golden/make_boundary_ties.py``): each is a ``boundary`` event
+    whose GPU path is exactly the best closed path through its boundary
+    state, and whose margin is within FP32 rounding of a tie -- while the
+    read costs alone (the states whose own survivors trace to the GPU's
+    boundary state) are percent-level away, so a margin that dropped the
+    through-path term would reject these ties."""
+
+    from pathlib import Path
+
+    from oracle import viterbi as ov
+
+    z = np.load(Path(__file__).parent / "golden" / "boundary_ties_k3.npz")
+    t, g, c = z["targets"], z["gpu_states"], z["cpu_states"]
+    n = len(t)
+    assert n >= 3
+    cpu = {"states": c[None], "targets": t[None]}
+    bits = np.full((1, n), 3)
+    stats = oenc.compare_states(g[None], cpu, {3: LABELS[3]}, bits, {3: 1})
+    assert stats["kinds"] == ["boundary"] * n
+    assert all(d == 0.0 for d in stats["sse_rel_deltas"])
+    # 0 where the two costs are equal in FP32 on this target (the lowest-index rule chose the CPU's state)
+    assert all(0.0 <= m <= 1e-6 for m in stats["boundary_margins"])
+    for i in range(n):
+        cost, _, end_of = ov.boundary_view(t[i], LABELS[3], K=3, boundary_lag=1)
+        own = end_of == (int(g[i, 0]) >> 3)
+        gap = (cost[own].min() - cost.min()) / cost.min() if own.any() else np.inf
+        assert gap > 1e-4

@@ -126,3 +126,83 @@ def test_vector_path_equals_scalar_path(K):
         assert np.array_equal(big_v[1], big_s[1])
         if small_v is not None:
             assert np.array_equal(small_v[1], small_s[1])
+
+
+# boundary views: tiny trellises where every state can be enumerated
+BOUNDARY_SMALL = [(6, 2, 8, 2), (6, 2, 8, 4), (6, 3, 6, 3), (4, 1, 8, 4), (8, 2, 6, 3), (10, 5, 3, 1)]
+
+
+@pytest.mark.parametrize("lag", (0, 1))
+@pytest.mark.parametrize(("L", "K", "T", "C"), BOUNDARY_SMALL)
+def test_boundary_view_matches_exhaustive_search(L, K, T, C, lag):
+    """Read costs, final costs and each state's traced end_state against
+    enumeration (ties exercised by the small integer alphabet); the encode's
+    own boundary is end_of at the lowest minimum of the read costs."""
+
+    rng = np.random.default_rng(7 * L + 3 * K + T + C + lag)
+    for _ in range(3):
+        lab = rng.integers(-3, 4, size=1 << L).astype(np.float32)
+        x = rng.integers(-4, 5, size=T).astype(np.float32)
+        cost, final, end_of = ov.boundary_view(x, lab, K=K, L=L, context=C, boundary_lag=lag)
+        b_cost, b_final, b_end = ov.brute_force_boundary(x, lab, K=K, L=L, context=C, boundary_lag=lag)
+        np.testing.assert_array_equal(cost, b_cost)
+        np.testing.assert_array_equal(final, b_final)
+        np.testing.assert_array_equal(end_of, b_end)
+        _, _, boundary = ov.encode(x[None], lab, K=K, L=L, context=C, boundary_lag=lag, return_boundary=True)
+        assert boundary[0] == end_of[int(np.argmin(cost))]
+
+
+@pytest.mark.parametrize(("L", "K", "T", "C"), BOUNDARY_SMALL)
+def test_primer_through_matches_exhaustive_search(L, K, T, C):
+    """Costs through every boundary state against enumeration; the minimum
+    over boundary states is the free primer's final cost, reached exactly at
+    each state's own traced end_state."""
+
+    rng = np.random.default_rng(11 * L + 5 * K + T + C)
+    lab = rng.integers(-3, 4, size=1 << L).astype(np.float32)
+    x = rng.integers(-4, 5, size=T).astype(np.float32)
+    S = 1 << (L - K)
+    _, final, end_of = ov.boundary_view(x, lab, K=K, L=L, context=C)
+    through = np.stack([ov.primer_through(x, lab, e, K=K, L=L, context=C) for e in range(S)])
+    for e in range(S):
+        np.testing.assert_array_equal(through[e], ov.brute_force_through(x, lab, e, K=K, L=L, context=C))
+    np.testing.assert_array_equal(through.min(axis=0), final)
+    np.testing.assert_array_equal(through[end_of, np.arange(S)], final)
+
+
+@pytest.mark.parametrize(("L", "K", "T", "C"), BOUNDARY_SMALL)
+def test_encode_from_matches_exhaustive_search_and_encode(L, K, T, C):
+    """The constrained pass from a given boundary state against enumeration;
+    from the encode's own boundary state it reproduces the encode."""
+
+    rng = np.random.default_rng(13 * L + 7 * K + T + C)
+    S = 1 << (L - K)
+    lab = rng.integers(-3, 4, size=1 << L).astype(np.float32)
+    xs = rng.integers(-4, 5, size=(4, T)).astype(np.float32)
+    ends = rng.integers(0, S, size=4)
+    recon, states = ov.encode_from(xs, lab, ends, K=K, L=L)
+    for i in range(4):
+        b_recon, b_states = ov.brute_force_from(xs[i], lab, int(ends[i]), K=K, L=L)
+        np.testing.assert_array_equal(states[i], b_states)
+        np.testing.assert_array_equal(recon[i], b_recon)
+    e_recon, e_states, boundary = ov.encode(xs, lab, K=K, L=L, context=C, return_boundary=True)
+    f_recon, f_states = ov.encode_from(xs, lab, boundary, K=K, L=L)
+    np.testing.assert_array_equal(f_states, e_states)
+    np.testing.assert_array_equal(f_recon, e_recon)
+
+
+def test_boundary_views_at_production_size():
+    """L16 K3 with the frozen table: the traced end_state of the read-cost
+    argmin is the encode's, and the cost through it equals the final cost of
+    that state bit for bit (the primer's own operations)."""
+
+    rng = np.random.default_rng(5)
+    lab = otables.t12_values(3)
+    x = rng.standard_normal(256).astype(np.float32)
+    cost, final, end_of = ov.boundary_view(x, lab, K=3, boundary_lag=1)
+    _, _, boundary = ov.encode(x[None], lab, K=3, boundary_lag=1, return_boundary=True)
+    s = int(np.argmin(cost))
+    assert end_of[s] == boundary[0]
+    through = ov.primer_through(x, lab, int(boundary[0]), K=3)
+    assert through[s] == final[s]
+    assert np.all(through >= final)
