@@ -173,6 +173,17 @@ def test_bf16_split_last_round(K, M, N, sym):
     if sym:
         assert torch.equal(split, split.T)
     assert not torch.equal(split, whole) or K < 128  # the split tiles did take the partial path
+    # only the last round's tiles changed path: every other tile is the unsplit kernel's, bit for bit,
+    # whichever wave of workgroups ran it
+    tm, tn = -(-M // 256), -(-N // 256)
+    tiles = tm * (tm + 1) // 2 if sym else tm * tn
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    pad = torch.zeros(tm * 256, tn * 256, dtype=torch.bool, device="cuda")
+    pad[:M, :N] = split != whole
+    moved = pad.view(tm, 256, tn, 256).any(dim=3).any(dim=1)
+    if sym:
+        moved = torch.triu(moved)
+    assert int(moved.sum()) <= tiles % cus
 
 
 def test_gemm_rejects_bad_arguments():
