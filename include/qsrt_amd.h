@@ -252,6 +252,22 @@ int qsrt_gemm_tn_ws(float *C, const void *A, const void *B, const void *B2, int6
                     size_t workspace_bytes, void *stream);
 
 /*
+ * Diagonal-block step of a blocked float64 Cholesky factorisation, for
+ * `batch` matrices A[b] = A + b * batch_stride (n x n, row-major, leading
+ * dimension n).  The lower triangle of the nb x nb block at (j0, j0) is
+ * factored in place (L11, zeros written above its diagonal) and L11^-1 is
+ * written to inv[b] (nb x nb row-major, zeros above the diagonal), so the
+ * caller's panel solve and trailing update are two DGEMMs.  A pivot that is
+ * not positive sets info[b] (int32, device) to j0 + k + 1, the order of the
+ * failing leading minor as LAPACK reports it, unless info[b] is already
+ * non-zero; that block is then undefined.  nb <= 128.  Replaces the
+ * factorisation inside block_ldl (qsrt/exl3_encoder_backend.py:323-393),
+ * which the reference runs as torch.linalg.cholesky in FP32.
+ */
+int qsrt_chol_diag_block_f64(double *A, int64_t n, int64_t batch, int64_t batch_stride, int64_t j0, int nb,
+                             double *inv, int32_t *info, void *stream);
+
+/*
  * BlockLDLQ step, batched over B members (member m quantizes source
  * src[m]).  For the 16-row block [blk, blk + 16) of a span ending at row
  * `end`, every member's target

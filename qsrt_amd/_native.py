@@ -66,6 +66,9 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float,
          _c_int, _c_void_p, _c_size, _c_void_p],
     ),
+    "qsrt_chol_diag_block_f64": (
+        _c_int, [_c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_void_p, _c_void_p, _c_void_p],
+    ),
     "qsrt_ldlq_targets": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64,
