@@ -166,6 +166,21 @@ def test_config3_strip_matches_cpu_encode():
     _check_matrix("config 3 strip", W, (xd.T @ xd).float(), rows, 3, default_qsrt_transform_seeds(1, "w1"))
 
 
+def test_config4_gate_full_size_matches_cpu_encode():
+    """BASELINE config 4 at full size: the 7168 x 2048 gate matrix at K2
+    (57,344 tiles, 448 BlockLDLQ steps) under H13 from the config's 16,384
+    AR(1) rows (rho 0.85), against the untethered CPU encode of the same
+    inputs.  H13 is summed in float64 on the device and handed to both sides
+    as FP32."""
+
+    d = bench.config_expert(4, DEV)
+    xd = d["x"].double()
+    H_sum = (xd.T @ xd).float().cpu()
+    del xd
+    _check_matrix("config 4 gate (full size)", d["w_gate"].T.contiguous().cpu(), H_sum, d["x"].shape[0], 2,
+                  default_qsrt_transform_seeds(1, "w1"))
+
+
 def test_few_row_hessian_matches_cpu_encode():
     """A Hessian from 48 calibration rows (rank 48 of 256 plus 1% damping, the
     conditioning of a rarely routed expert): the device factorisation must
