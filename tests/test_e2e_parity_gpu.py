@@ -181,6 +181,19 @@ def test_config4_gate_full_size_matches_cpu_encode():
                   default_qsrt_transform_seeds(1, "w1"))
 
 
+def test_config3_gate_full_size_matches_cpu_encode():
+    """BASELINE config 3 at full size: the 5120 x 1536 gate matrix at K3
+    (30,720 tiles) under H13 from the config's 8192 AR(1) rows (rho 0.9)
+    with 8 outlier channels at 20x variance."""
+
+    d = bench.config_expert(3, DEV)
+    xd = d["x"].double()
+    H_sum = (xd.T @ xd).float().cpu()
+    del xd
+    _check_matrix("config 3 gate (full size)", d["w_gate"].T.contiguous().cpu(), H_sum, d["x"].shape[0], 3,
+                  default_qsrt_transform_seeds(1, "w1"))
+
+
 def test_few_row_hessian_matches_cpu_encode():
     """A Hessian from 48 calibration rows (rank 48 of 256 plus 1% damping, the
     conditioning of a rarely routed expert): the device factorisation must
