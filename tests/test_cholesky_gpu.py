@@ -109,3 +109,40 @@ def test_block_ldl_retries_an_indefinite_matrix():
     assert not torch.equal(H, A)  # the retry damped it
     assert torch.equal(L.tril(), L)
     assert int(torch.linalg.cholesky_ex(H)[1]) == 0
+
+
+def test_diagonal_block_batched_with_an_indefinite_member():
+    """Three matrices in one launch (batch stride n * n): each member's block
+    is its own factor and inverse, and a member made indefinite reports its
+    own info without touching the others'."""
+
+    n, j0, nb, batch = 256, 128, 128, 3
+    A = torch.stack([_spd(n, 40 + b) for b in range(batch)])
+    A[1, j0 + 7, j0 + 7] = -1.0
+    M = A.clone()
+    inv = torch.zeros(batch, nb, nb, dtype=torch.float64, device=DEV)
+    info = torch.zeros(batch, dtype=torch.int32, device=DEV)
+    lib = _native.lib()
+    _native.check(lib.qsrt_chol_diag_block_f64(M.data_ptr(), n, batch, n * n, j0, nb, inv.data_ptr(),
+                                                info.data_ptr(), _native.stream_handle(DEV)), "chol")
+    torch.cuda.synchronize()
+    assert info.tolist() == [0, j0 + 8, 0]
+    eye = torch.eye(nb, dtype=torch.float64, device=DEV)
+    for b in (0, 2):
+        blk = M[b, j0:j0 + nb, j0:j0 + nb]
+        ref = torch.linalg.cholesky(A[b, j0:j0 + nb, j0:j0 + nb])
+        assert (blk - ref).abs().max().item() <= 1e-13 * ref.abs().max().item()
+        assert (blk @ inv[b] - eye).abs().max().item() <= 1e-12
+
+
+def test_bad_arguments_are_rejected():
+    lib = _native.lib()
+    A = torch.zeros(4, 4, dtype=torch.float64, device=DEV)
+    inv = torch.zeros(4, 4, dtype=torch.float64, device=DEV)
+    info = torch.zeros(1, dtype=torch.int32, device=DEV)
+    s = _native.stream_handle(DEV)
+    for args in ((4, 1, 16, 0, 129), (4, 1, 16, 2, 3), (4, 1, 16, -1, 2), (4, 2, 8, 0, 2), (0, 1, 0, 0, 1)):
+        n, batch, stride, j0, nb = args
+        with pytest.raises(ValueError):
+            _native.check(lib.qsrt_chol_diag_block_f64(A.data_ptr(), n, batch, stride, j0, nb, inv.data_ptr(),
+                                                        info.data_ptr(), s), "chol")
