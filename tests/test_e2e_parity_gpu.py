@@ -194,6 +194,23 @@ def test_config3_gate_full_size_matches_cpu_encode():
                   default_qsrt_transform_seeds(1, "w1"))
 
 
+def test_config5_rarely_routed_expert_full_size_matches_cpu_encode():
+    """BASELINE config 5's hardest conditioning at full size: the gate
+    matrix (7168 x 2048, K3) of a layer expert that the Zipf routing gives
+    only 19 of 65,536 calibration rows, so H13 is rank 19 plus the 1%
+    damping.  An FP32 factorisation of it would move decisions against any
+    other; the float64 one keeps the payload to near ties."""
+
+    counts = bench.zipf_token_counts()
+    expert = counts.index(min(counts))
+    d = bench.config_expert(5, DEV, expert=expert, tokens=counts[expert])
+    xd = d["x"].double()
+    H_sum = (xd.T @ xd).float().cpu()
+    del xd
+    _check_matrix(f"config 5 expert {expert} gate ({counts[expert]} rows)", d["w_gate"].T.contiguous().cpu(), H_sum,
+                  d["x"].shape[0], 3, default_qsrt_transform_seeds(1, "w1"))
+
+
 def test_few_row_hessian_matches_cpu_encode():
     """A Hessian from 48 calibration rows (rank 48 of 256 plus 1% damping, the
     conditioning of a rarely routed expert): the device factorisation must
