@@ -70,6 +70,8 @@ def _load():
             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
         ]
+        lib.qsrt_oracle_default_threads.restype = ctypes.c_int
+        lib.qsrt_oracle_default_threads.argtypes = []
         lib.qsrt_oracle_set_vector.restype = None
         lib.qsrt_oracle_set_vector.argtypes = [ctypes.c_int]
         _lib = lib

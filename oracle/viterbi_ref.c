@@ -64,6 +64,16 @@ static int vt_use_vector = 1;
 
 void qsrt_oracle_set_vector(int enable) { vt_use_vector = enable != 0; }
 
+/* The OpenMP team size a call with n_threads = 0 uses (1 without OpenMP). */
+int qsrt_oracle_default_threads(void)
+{
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
 #ifdef __AVX2__
 /* predecessor costs of states s0 .. s0+7 (s0 a multiple of 8) for choice k */
 static inline __m256 vt_pred8(const float *prev, int k, int q0, int K, int pred_shift)
@@ -231,12 +241,15 @@ int qsrt_oracle_viterbi(const float *tiles, float *recon, uint16_t *states, int6
         (boundary_lag != 0 && boundary_lag != 1) || n_tiles < 0)
         return -1;
     int failed = 0;
+    /* the thread count applies to this call's parallel region only (omp_set_num_threads would change the
+     * process-wide default for every later call that passes 0) */
 #ifdef _OPENMP
-    if (n_threads > 0) omp_set_num_threads(n_threads);
+    const int team = n_threads > 0 ? n_threads : omp_get_max_threads();
 #else
+    const int team = 1;
     (void)n_threads;
 #endif
-#pragma omp parallel reduction(| : failed)
+#pragma omp parallel num_threads(team) reduction(| : failed)
     {
         vt_ctx c;
         if (!vt_ctx_init(&c, L, K, T)) failed = 1;
@@ -333,12 +346,15 @@ int qsrt_oracle_viterbi_from(const float *tiles, float *recon, uint16_t *states,
     for (int64_t t = 0; t < n_tiles; ++t)
         if (end_states[t] < 0 || end_states[t] >= (1 << (L - K))) return -1;
     int failed = 0;
+    /* the thread count applies to this call's parallel region only (omp_set_num_threads would change the
+     * process-wide default for every later call that passes 0) */
 #ifdef _OPENMP
-    if (n_threads > 0) omp_set_num_threads(n_threads);
+    const int team = n_threads > 0 ? n_threads : omp_get_max_threads();
 #else
+    const int team = 1;
     (void)n_threads;
 #endif
-#pragma omp parallel reduction(| : failed)
+#pragma omp parallel num_threads(team) reduction(| : failed)
     {
         vt_ctx c;
         if (!vt_ctx_init(&c, L, K, T)) failed = 1;

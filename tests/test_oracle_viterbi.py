@@ -206,3 +206,17 @@ def test_boundary_views_at_production_size():
     through = ov.primer_through(x, lab, int(boundary[0]), K=3)
     assert through[s] == final[s]
     assert np.all(through >= final)
+
+
+def test_a_thread_count_applies_to_its_own_call_only():
+    """``threads=1`` on one call must not shrink the team of later calls that
+    pass 0 (the default): the count is a per-call clause, not a change of the
+    process-wide OpenMP default."""
+
+    lib = ov._load()
+    before = lib.qsrt_oracle_default_threads()
+    x = np.zeros((2, 8), dtype=np.float32)
+    lab = np.zeros(1 << 6, dtype=np.float32)
+    ov.encode(x, lab, K=2, L=6, context=2, threads=1)
+    ov.encode_from(x, lab, [0, 1], K=2, L=6, threads=1)
+    assert lib.qsrt_oracle_default_threads() == before
