@@ -19,7 +19,8 @@ def _rel(got, want):
     return float(np.max(np.abs(got - want)) / max(np.abs(want).max(), 1e-30))
 
 
-@pytest.mark.parametrize("M,N,K", [(16, 256, 112), (200, 300, 77), (128, 128, 16), (1, 5, 3), (640, 4096, 128)])
+@pytest.mark.parametrize("M,N,K", [(16, 256, 112), (200, 300, 77), (128, 128, 16), (1, 5, 3), (640, 4096, 128),
+                                   (96, 200, 129), (300, 260, 1000)])
 def test_fused_feedback_product_matches_float64(M, N, K):
     print(f"[gemm] f32 M{M} N{N} K{K}", file=sys.stderr, flush=True)
     g = torch.Generator().manual_seed(M * 7 + N + K)
