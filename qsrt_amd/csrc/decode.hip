@@ -237,7 +237,11 @@ void decode_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t total_block
     __syncthreads();
 
     for (int64_t blk = begin; blk < end; ++blk) {
-        // ---- A: stage the tile-column's words, decode the lane's labels
+        // ---- A: stage the tile-column's words, decode the lane's labels.  From here to the end of B1 the wave
+        // runs at raised issue priority and drops back for B2: a wave in its right product and stores then
+        // yields issue slots to waves still gathering labels or in the left product, so the two workgroups'
+        // phases overlap better (bit-identical output; 0.82-0.86 ms against 0.89-0.96 ms on 96 K3 matrices).
+        __builtin_amdgcn_s_setprio(2);
         if (lane < 16 * K) reinterpret_cast<u32x4*>(slice)[lane] = words;
         uint32_t lab[8];
 #pragma unroll
@@ -301,6 +305,7 @@ void decode_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t total_block
             e[a2] = acc;
         }
         __syncthreads();  // every wave is done reading labels: slices are private again
+        __builtin_amdgcn_s_setprio(0);
 
         // ---- B2: right H8 across tile-columns (exact on the fp8 path)
 #pragma unroll
