@@ -882,6 +882,88 @@ def hadamard_bench(steps: int = 5):
     return {"workload": f"[{k} x {n}] f32, block 128, fused signs, in place", **out}
 
 
+def _bakron_band_flops(ob: int, ib: int, first: int, middle: int, last: int) -> int:
+    """Algorithmic flops of one fused band update: 2 * 16^3 per (target block,
+    source block) pair of the left and right products."""
+
+    pairs = 0
+    for d in range(first, last):
+        for o in range(max(0, d - ib + 1), min(ob, d + 1)):
+            i = d - o
+            pairs += max(0, min(ob, middle - i) - max(0, first - i))
+            if d >= middle:
+                pairs += max(0, min(ib, middle, last - o) - max(0, first - o))
+    return 2 * 16 ** 3 * pairs
+
+
+def bakron_bench(steps: int = 5):
+    """BaKron band propagation on the config-4 gate (weights [7168, 2048] in
+    the encoder orientation: 2048 output x 7168 input rows of 16 x 16 blocks,
+    575 anti-diagonals).  The top band of the divide and conquer (diagonals
+    [0, 287) into [287, 575)) is the roofline line (FP32 matrix cores); the
+    whole recursion's 574 band updates are timed back to back, on the HIP
+    kernel and on the bounding-box torch products."""
+
+    from qsrt_amd.sqg_quantizer import apply_bakron_block_update
+    from qsrt_amd.two_sided_rounding import _propagate_band
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(20261201 + 11)
+    n_out, n_in = 2048, 7168
+    ob, ib = n_out // 16, n_in // 16
+    diagonals = ob + ib - 1
+    T = torch.randn((n_out, n_in), device=dev, generator=g)
+    Q = torch.round(T * 4) / 4
+    l_out = torch.randn((n_out, n_out), device=dev, generator=g) / n_out ** 0.5
+    l_in = torch.randn((n_in, n_in), device=dev, generator=g) / n_in ** 0.5
+    l_out = l_out * torch.kron(torch.tril(torch.ones(ob, ob, device=dev)), torch.ones(16, 16, device=dev))
+    l_in = l_in * torch.kron(torch.tril(torch.ones(ib, ib, device=dev)), torch.ones(16, 16, device=dev))
+    inter = torch.empty_like(T)
+    bands = []
+
+    def rec(first, last):
+        if last == first + 1:
+            return
+        mid = (first + last) // 2
+        rec(first, mid)
+        bands.append((first, mid, last))
+        rec(mid, last)
+
+    rec(0, diagonals)
+    top = (0, diagonals // 2, diagonals)
+
+    def hip(band):
+        apply_bakron_block_update(T, Q, l_out, l_in, inter, first_diagonal=band[0], middle_diagonal=band[1],
+                                  last_diagonal=band[2], block_size=16)
+
+    top_ms = _time_ms(lambda: hip(top), steps)
+    top_flops = _bakron_band_flops(ob, ib, *top)
+    achieved = top_flops / (top_ms / 1e3) / 1e12
+
+    def all_hip():
+        for band in bands:
+            hip(band)
+
+    def all_torch():
+        for band in bands:
+            _propagate_band(T, Q, l_out, l_in, first=band[0], middle=band[1], last=band[2], block_size=16)
+
+    all_ms = _time_ms(all_hip, 2, min_ms=0.0, warm_ms=0.0)
+    all_flops = sum(_bakron_band_flops(ob, ib, *b) for b in bands)
+    torch_ms = _time_ms(all_torch, 2, min_ms=0.0, warm_ms=0.0)
+    del T, Q, l_out, l_in, inter
+    torch.cuda.empty_cache()
+    return {"workload": f"{n_out} x {n_in} FP32 (config-4 gate, encoder orientation), 16 x 16 blocks, "
+                        f"{diagonals} anti-diagonals",
+            "kernel": "bakron_left_kernel + bakron_right_kernel",
+            "top_band": {"diagonals": list(top), "ms": round(top_ms, 4), "roofline": {
+                "bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "traffic": None,
+                "algorithmic": f"2 x 16^3 flops per (target, source) block pair x {top_flops // 8192} pairs"}},
+            "recursion": {"bands": len(bands), "hip_ms": round(all_ms, 3), "torch_bounding_box_ms": round(torch_ms, 3),
+                          "hip_tflops": round(all_flops / (all_ms / 1e3) / 1e12, 2)}}
+
+
 def copy_calibration(nbytes: int) -> None:
     """A plain device copy of ``nbytes`` (the known-size reference for the
     HBM byte counters)."""
@@ -894,7 +976,7 @@ def copy_calibration(nbytes: int) -> None:
     log(f"[bench] copied {nbytes} bytes")
 
 
-LINES = ("layer", "microbench", "expert", "glm", "k2", "gemm", "hadamard")
+LINES = ("layer", "microbench", "expert", "glm", "k2", "gemm", "hadamard", "bakron")
 
 
 def headline(lay: dict, warmup: int) -> dict:
@@ -1044,6 +1126,9 @@ def main() -> int:
     if "hadamard" in lines:
         log("[bench] Hadamard kernel")
         result["hadamard"] = hadamard_bench()
+    if "bakron" in lines:
+        log("[bench] BaKron band update")
+        result["bakron"] = bakron_bench()
     print(json.dumps(result), flush=True)
     return 0
 

@@ -268,6 +268,29 @@ int qsrt_chol_diag_block_f64(double *A, int64_t n, int64_t batch, int64_t batch_
                              double *inv, int32_t *info, void *stream);
 
 /*
+ * One band propagation of the recursive BaKron two-sided rounding, FP32,
+ * 16 x 16 blocks.  workspace (T), quantized (Q) and intermediate (I) are
+ * [batch, n_out, n_in] row-major; output_factor and input_factor are
+ * [n_out, n_out] and [n_in, n_in] per member at the given batch strides (0:
+ * one factor shared by every member).  With block (o, i) on anti-diagonal
+ * o + i, ob = n_out / 16, ib = n_in / 16 and the diagonals
+ * 0 <= first < middle < last <= ob + ib - 1:
+ *   I(o, i)  = sum_{s in [max(0, first - i), min(ob, middle - i))} Lout(o, s) (Q - T)(s, i)
+ *              for first <= o + i < last;
+ *   T(o, c) += sum_{s in [max(0, first - o), min(ib, middle, last - o))} I(o, s) Lin(c, s)^T
+ *              for middle <= o + c < last.
+ * Other blocks of T and I are not touched.  n_out and n_in are positive
+ * multiples of 16 with n_out * n_in <= 2^31, batch <= 65535.  Replaces
+ * bakron_block_update_cuda (qsrt/csrc/sqg_quantize.cu:991-1100, kernels
+ * :141-270), bound as qsrt/sqg_quantizer.py:383-407.
+ */
+int qsrt_bakron_band_update_f32(float *workspace, const float *quantized, const float *output_factor,
+                                const float *input_factor, float *intermediate, int64_t batch, int64_t n_out,
+                                int64_t n_in, int64_t output_factor_batch_stride, int64_t input_factor_batch_stride,
+                                int64_t first_diagonal, int64_t middle_diagonal, int64_t last_diagonal,
+                                void *stream);
+
+/*
  * BlockLDLQ step, batched over B members (member m quantizes source
  * src[m]).  For the 16-row block [blk, blk + 16) of a span ending at row
  * `end`, every member's target

@@ -250,3 +250,56 @@ def install_sqg_quantizer(quantizer_module) -> None:
 
     quantizer_module.quantize_tiles = quantize_tiles
     quantizer_module._qsrt_sqg_installed = True
+
+
+def apply_bakron_block_update(workspace: torch.Tensor, quantized: torch.Tensor, output_factor: torch.Tensor,
+                              input_factor: torch.Tensor, intermediate: torch.Tensor, *, first_diagonal: int,
+                              middle_diagonal: int, last_diagonal: int, block_size: int) -> None:
+    """One fused FP32 band propagation of the recursive BaKron rounding on the
+    GPU (reference ``qsrt/sqg_quantizer.py:383-407`` over
+    ``qsrt/csrc/sqg_quantize.cu:991-1100``): the intermediate receives
+    ``Lout (Q - T)`` restricted to the finished band [first, middle) on the
+    diagonals [first, last), and the workspace gains
+    ``intermediate Lin^T`` on the next band [middle, last).  Runs the HIP
+    kernel behind ``qsrt_bakron_band_update_f32`` on the current stream; the
+    checks and their messages follow the reference launcher's."""
+
+    if not workspace.is_cuda:
+        raise ValueError("workspace must be CUDA")
+    if workspace.dtype != torch.float32:
+        raise ValueError("workspace must be FP32")
+    if workspace.ndim not in (2, 3) or not workspace.is_contiguous():
+        raise ValueError("workspace must be a contiguous matrix or matrix batch")
+    if quantized.shape != workspace.shape or quantized.dtype != torch.float32 or not quantized.is_contiguous():
+        raise ValueError("quantized matrix must match workspace")
+    if (intermediate.shape != workspace.shape or intermediate.dtype != torch.float32
+            or not intermediate.is_contiguous()):
+        raise ValueError("intermediate matrix must match workspace")
+    for factor, name in ((output_factor, "output factor"), (input_factor, "input factor")):
+        if (not factor.is_cuda or factor.device != workspace.device or factor.dtype != torch.float32
+                or factor.ndim not in (2, 3) or not factor.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous CUDA FP32 matrix")
+    if quantized.device != workspace.device or intermediate.device != workspace.device:
+        raise ValueError("BaKron matrices must share one CUDA device")
+    if block_size != 16:
+        raise ValueError("fused BaKron updates require 16x16 blocks")
+    n_out, n_in = map(int, workspace.shape[-2:])
+    batch = 1 if workspace.ndim == 2 else int(workspace.shape[0])
+    if n_out % 16 or n_in % 16:
+        raise ValueError("BaKron dimensions must be divisible by 16")
+    if tuple(output_factor.shape[-2:]) != (n_out, n_out) or (output_factor.ndim == 3
+                                                            and output_factor.shape[0] != batch):
+        raise ValueError("output factor shape mismatch")
+    if tuple(input_factor.shape[-2:]) != (n_in, n_in) or (input_factor.ndim == 3 and input_factor.shape[0] != batch):
+        raise ValueError("input factor shape mismatch")
+    diagonals = n_out // 16 + n_in // 16 - 1
+    first, middle, last = int(first_diagonal), int(middle_diagonal), int(last_diagonal)
+    if not 0 <= first < middle < last <= diagonals:
+        raise ValueError("invalid recursive BaKron diagonal range")
+    lib = _native.lib()
+    with torch.cuda.device(workspace.device):
+        _native.check(lib.qsrt_bakron_band_update_f32(
+            workspace.data_ptr(), quantized.data_ptr(), output_factor.data_ptr(), input_factor.data_ptr(),
+            intermediate.data_ptr(), batch, n_out, n_in, 0 if output_factor.ndim == 2 else n_out * n_out,
+            0 if input_factor.ndim == 2 else n_in * n_in, first, middle, last,
+            _native.stream_handle(workspace.device)), "qsrt_bakron_band_update_f32")

@@ -15,7 +15,12 @@ quantizer keeps one legal path per tile.  Three equivalent recurrences:
   is propagated into the next band ``[middle, last)`` once, as two products
   restricted to the blocks the bands can reach.
 
-All products are dense FP32/FP64 tensor products on the tensors' device.
+On the GPU in FP32 with 16 x 16 blocks, every band propagation of the
+divide and conquer (and of the lockstep batches) is the fused HIP band
+kernel (``qsrt_amd.sqg_quantizer.apply_bakron_block_update``, two launches
+per band, one wave per target block on the FP32 matrix cores); otherwise,
+and for the anti-diagonal recurrence, the update is two dense tensor
+products on the bands' bounding boxes.
 """
 
 from __future__ import annotations
@@ -26,6 +31,7 @@ from dataclasses import dataclass
 import torch
 
 from .qsrt_coupled import block_hadamard
+from .sqg_quantizer import apply_bakron_block_update as _hip_apply_update
 from .two_sided_ldlq import two_sided_block_ldlq
 
 TileQuantizer = Callable[[torch.Tensor], tuple[torch.Tensor, torch.Tensor]]
@@ -248,15 +254,28 @@ def _propagate_band(workspace, quantized, output_factor, input_factor, *, first:
     workspace[..., tr0 * b:tr1 * b, tc0 * b:tc1 * b] += update * tmask
 
 
+def _hip_update_applies(workspace: torch.Tensor, work_dtype, block_size: int) -> bool:
+    return workspace.is_cuda and work_dtype == torch.float32 and block_size == 16
+
+
 def apply_bakron_block_update(workspace, quantized, output_factor, input_factor, intermediate=None, *,
                               first_diagonal: int, middle_diagonal: int, last_diagonal: int,
                               block_size: int = 16) -> None:
     """One band propagation of the recursive BaKron recurrence (the operation
-    the reference binds as ``qsrt.sqg_quantizer.apply_bakron_block_update``);
-    ``intermediate`` is accepted for signature parity and not needed."""
+    the reference binds as ``qsrt.sqg_quantizer.apply_bakron_block_update``).
+    GPU FP32 problems with 16 x 16 blocks run the fused HIP band kernel
+    (``intermediate`` is then the kernel's [.., n_out, n_in] buffer,
+    allocated here when None); others run the two bounding-box products."""
 
     if not first_diagonal < middle_diagonal < last_diagonal:
         raise ValueError("band diagonals must satisfy first < middle < last")
+    if _hip_update_applies(workspace, workspace.dtype, block_size):
+        if intermediate is None:
+            intermediate = torch.empty_like(workspace)
+        _hip_apply_update(workspace, quantized, output_factor, input_factor, intermediate,
+                          first_diagonal=first_diagonal, middle_diagonal=middle_diagonal,
+                          last_diagonal=last_diagonal, block_size=block_size)
+        return
     _propagate_band(workspace, quantized, output_factor, input_factor, first=first_diagonal, middle=middle_diagonal,
                     last=last_diagonal, block_size=block_size)
 
@@ -265,7 +284,8 @@ class _BakronState:
     """Reversed-order running targets, reconstructions and payload grid of
     one or a batch of matrices."""
 
-    def __init__(self, weights, input_factor, output_factor, input_reverse, output_reverse, block_size, work_dtype):
+    def __init__(self, weights, input_factor, output_factor, input_reverse, output_reverse, block_size, work_dtype,
+                 hip_update=False):
         self.b = block_size
         self.batched = weights.ndim == 3
         w = weights if self.batched else weights.unsqueeze(0)
@@ -278,6 +298,21 @@ class _BakronState:
         self.in_rev, self.out_rev = input_reverse, output_reverse
         self.payload = None
         self.dtype = work_dtype
+        self.intermediate = torch.empty_like(self.workspace) if hip_update else None
+
+    def propagate(self, first: int, middle: int, last: int) -> None:
+        """Band [first, middle) into [middle, last): the fused HIP kernel when
+        the state was built for it, the bounding-box products otherwise."""
+
+        if self.intermediate is not None:
+            l_out = self.l_out[0] if self.l_out.ndim == 3 and self.l_out.shape[0] == 1 else self.l_out
+            l_in = self.l_in[0] if self.l_in.ndim == 3 and self.l_in.shape[0] == 1 else self.l_in
+            _hip_apply_update(self.workspace, self.quantized, l_out.contiguous(), l_in.contiguous(),
+                              self.intermediate, first_diagonal=first, middle_diagonal=middle,
+                              last_diagonal=last, block_size=self.b)
+        else:
+            _propagate_band(self.workspace, self.quantized, self.l_out, self.l_in, first=first, middle=middle,
+                            last=last, block_size=self.b)
 
     def _blocks(self, x):
         return x.view(self.batch, self.ob, self.b, self.ib, self.b).permute(0, 1, 3, 2, 4)
@@ -336,8 +371,7 @@ def _recurse(st: _BakronState, quantize_tiles, first: int, last: int) -> None:
         return
     middle = (first + last) // 2
     _recurse(st, quantize_tiles, first, middle)
-    _propagate_band(st.workspace, st.quantized, st.l_out, st.l_in, first=first, middle=middle, last=last,
-                    block_size=st.b)
+    st.propagate(first, middle, last)
     _recurse(st, quantize_tiles, middle, last)
 
 
@@ -348,21 +382,25 @@ def bakron_block_round_encoder(weight: torch.Tensor, input_hessian: torch.Tensor
     """Two-sided adaptive rounding by BaKron's divide and conquer over
     anti-diagonals: one quantizer call per anti-diagonal, every band pair
     propagated once (reference :655-820).  ``update_chunk_blocks`` is
-    validated for interface parity (the band products are not chunked);
-    ``update_backend`` ``"cuda"`` requires a GPU FP32 16x16 problem, as the
-    reference's."""
+    validated for interface parity (the band products are not chunked).
+    ``update_backend`` as the reference's (:707-715): ``"auto"`` runs the
+    fused HIP band kernel for a GPU FP32 problem with 16x16 blocks and the
+    bounding-box products otherwise, ``"torch"`` always the products,
+    ``"cuda"`` requires the kernel's conditions."""
 
     _check_weight_and_hessians(weight, input_hessian, output_hessian, block_size, work_dtype)
     if update_chunk_blocks <= 0:
         raise ValueError("update_chunk_blocks must be positive")
     if update_backend not in ("auto", "torch", "cuda"):
         raise ValueError("update_backend must be 'auto', 'torch', or 'cuda'")
-    if update_backend == "cuda" and not (weight.is_cuda and work_dtype == torch.float32 and block_size == 16):
+    hip_update = update_backend == "cuda" or (update_backend == "auto"
+                                              and _hip_update_applies(weight, work_dtype, block_size))
+    if update_backend == "cuda" and not _hip_update_applies(weight, work_dtype, block_size):
         raise ValueError("GPU BaKron updates require a GPU FP32 problem with 16x16 blocks")
     device = weight.device
     l_in, in_rev = _unit_block_inverse_cholesky_factor(input_hessian, block_size, dtype=work_dtype, device=device)
     l_out, out_rev = _unit_block_inverse_cholesky_factor(output_hessian, block_size, dtype=work_dtype, device=device)
-    st = _BakronState(weight, l_in, l_out, in_rev, out_rev, block_size, work_dtype)
+    st = _BakronState(weight, l_in, l_out, in_rev, out_rev, block_size, work_dtype, hip_update)
     _recurse(st, quantize_tiles, 0, st.ob + st.ib - 1)
     return st.result(weight.dtype)
 
@@ -404,7 +442,7 @@ def bakron_block_round_encoder_batch(weights: torch.Tensor, input_hessians: torc
     outs = [_unit_block_inverse_cholesky_factor(output_hessians[j], block_size, dtype=work_dtype, device=device)
             for j in range(batch)]
     st = _BakronState(weights, torch.stack([f for f, _ in ins]), torch.stack([f for f, _ in outs]), ins[0][1],
-                      outs[0][1], block_size, work_dtype)
+                      outs[0][1], block_size, work_dtype, hip_update=True)
     _recurse(st, quantize_tiles, 0, st.ob + st.ib - 1)
     return st.result(weights.dtype)
 
@@ -428,7 +466,8 @@ def bakron_block_round_encoder_prepared_batch(weights: torch.Tensor, input_facto
     for reverse, dim, name in ((input_reverse, k, "input reverse order"), (output_reverse, n, "output reverse order")):
         if tuple(reverse.shape) != (dim,) or reverse.device != weights.device or reverse.dtype != torch.long:
             raise ValueError(f"{name} has incompatible geometry")
-    st = _BakronState(weights, input_factors, output_factors, input_reverse, output_reverse, block_size, work_dtype)
+    st = _BakronState(weights, input_factors, output_factors, input_reverse, output_reverse, block_size, work_dtype,
+                      hip_update=True)
     _recurse(st, quantize_tiles, 0, st.ob + st.ib - 1)
     return st.result(weights.dtype)
 

@@ -41,15 +41,14 @@ def test_lockstep_batch_matches_independent_encodes():
     h_in = torch.stack((_spd(32, 8101), _spd(32, 8102))).to(DEV)
     h_out = torch.stack((_spd(48, 8103), _spd(48, 8104))).to(DEV)
     batched = bakron_block_round_encoder_batch(w, h_in, h_out, _round_tiles)
-    for j in range(2):
+    for j in range(2):  # both run the HIP band kernel ("auto" on a GPU FP32 problem): the same sums
         one = bakron_block_round_encoder(w[j], h_in[j], h_out[j], _round_tiles, work_dtype=torch.float32)
-        differ = float((one.payload != batched.payload[j]).float().mean())
-        assert differ <= 0.01, differ
+        assert torch.equal(one.payload, batched.payload[j])
     f_in, r_in = factor_bakron_hessian(h_in[0])
     f_out, r_out = factor_bakron_hessian(h_out[0])
     shared = bakron_block_round_encoder_prepared_batch(w, f_in, f_out, r_in, r_out, _round_tiles)
     one = bakron_block_round_encoder(w[1], h_in[0], h_out[0], _round_tiles, work_dtype=torch.float32)
-    assert float((one.payload != shared.payload[1]).float().mean()) <= 0.01
+    assert torch.equal(one.payload, shared.payload[1])
 
 
 def test_bakron_with_the_tile_viterbi():
