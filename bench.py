@@ -67,6 +67,9 @@ DECODE_TRAFFIC_OVER_ALGORITHMIC = 1.013
 # the fixup kernel of its K-split tiles together).
 GEMM_HBM_BYTES = {"hessian_capture": 2.435e9, "ldlq_span_update": 1.485e8}
 HADAMARD_HBM_BYTES = {"left": 1.1782e8, "right": 1.1765e8}
+# Same counters for the BaKron top band's left + right launches (profiles/bakron_band_kernels_config4_gate.md):
+# mostly the right product's re-reads of the input factor.
+BAKRON_TOP_BAND_HBM_BYTES = 5.520e9
 
 LAYER_EXPERTS = 384
 LAYER_TOKENS = 65536
@@ -958,7 +961,7 @@ def bakron_bench(steps: int = 5):
             "kernel": "bakron_left_kernel + bakron_right_kernel",
             "top_band": {"diagonals": list(top), "ms": round(top_ms, 4), "roofline": {
                 "bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "traffic": None,
+                "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "traffic": round(BAKRON_TOP_BAND_HBM_BYTES),
                 "algorithmic": f"2 x 16^3 flops per (target, source) block pair x {top_flops // 8192} pairs"}},
             "recursion": {"bands": len(bands), "hip_ms": round(all_ms, 3), "torch_bounding_box_ms": round(torch_ms, 3),
                           "hip_tflops": round(all_flops / (all_ms / 1e3) / 1e12, 2)}}
