@@ -252,6 +252,11 @@ def install_sqg_quantizer(quantizer_module) -> None:
     quantizer_module._qsrt_sqg_installed = True
 
 
+def _overlap(a: torch.Tensor, b: torch.Tensor) -> bool:
+    a0, b0 = a.data_ptr(), b.data_ptr()
+    return a0 < b0 + b.numel() * b.element_size() and b0 < a0 + a.numel() * a.element_size()
+
+
 def apply_bakron_block_update(workspace: torch.Tensor, quantized: torch.Tensor, output_factor: torch.Tensor,
                               input_factor: torch.Tensor, intermediate: torch.Tensor, *, first_diagonal: int,
                               middle_diagonal: int, last_diagonal: int, block_size: int) -> None:
@@ -281,6 +286,15 @@ def apply_bakron_block_update(workspace: torch.Tensor, quantized: torch.Tensor, 
             raise ValueError(f"{name} must be a contiguous CUDA FP32 matrix")
     if quantized.device != workspace.device or intermediate.device != workspace.device:
         raise ValueError("BaKron matrices must share one CUDA device")
+    # the left launch writes the intermediate while reading the others, the right one writes the workspace
+    for other, name in ((workspace, "workspace"), (quantized, "quantized matrix"), (output_factor, "output factor"),
+                        (input_factor, "input factor")):
+        if _overlap(intermediate, other):
+            raise ValueError(f"intermediate matrix must not overlap the {name}")
+    for other, name in ((quantized, "quantized matrix"), (output_factor, "output factor"),
+                        (input_factor, "input factor")):
+        if _overlap(workspace, other):
+            raise ValueError(f"workspace must not overlap the {name}")
     if block_size != 16:
         raise ValueError("fused BaKron updates require 16x16 blocks")
     n_out, n_in = map(int, workspace.shape[-2:])

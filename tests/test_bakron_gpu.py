@@ -13,7 +13,6 @@ reference's tests/test_two_sided_rounding.py:244-326)."""
 
 from __future__ import annotations
 
-import ctypes
 import sys
 
 import numpy as np
@@ -135,15 +134,31 @@ def test_every_band_of_a_recursion_matches_the_oracle():
 
 def test_the_c_abi_rejects_bad_arguments():
     lib = _native.lib()
-    ws = torch.zeros((64, 96), device=DEV)
+    ws, q, inter = (torch.zeros((64, 96), device=DEV) for _ in range(3))
     f_out, f_in = torch.eye(64, device=DEV), torch.eye(96, device=DEV)
-    p = [ws.data_ptr(), ws.data_ptr(), f_out.data_ptr(), f_in.data_ptr(), ws.data_ptr()]
+    p = [ws.data_ptr(), q.data_ptr(), f_out.data_ptr(), f_in.data_ptr(), inter.data_ptr()]
     s = _native.stream_handle(DEV)
     assert lib.qsrt_bakron_band_update_f32(*p, 1, 64, 96, 0, 0, 0, 4, 9, s) == 0
     for args in ((1, 64, 96, 0, 0, 0, 4, 10), (1, 64, 96, 0, 0, 4, 4, 9), (1, 64, 90, 0, 0, 0, 4, 9),
                  (0, 64, 96, 0, 0, 0, 4, 9), (2, 64, 96, 100, 0, 0, 4, 9), (1, 64, 96, 0, 0, -1, 4, 9)):
         assert lib.qsrt_bakron_band_update_f32(*p, *args, s) == -1, args
     assert lib.qsrt_bakron_band_update_f32(None, *p[1:], 1, 64, 96, 0, 0, 0, 4, 9, s) == -1
+    torch.cuda.synchronize()
+
+
+def test_overlapping_buffers_are_rejected():
+    ws = torch.zeros((64, 96), device=DEV)
+    q = torch.zeros_like(ws)
+    f_out, f_in = torch.eye(64, device=DEV), torch.eye(96, device=DEV)
+    big = torch.zeros((2, 64, 96), device=DEV)
+    kw = dict(first_diagonal=0, middle_diagonal=4, last_diagonal=9, block_size=16)
+    with pytest.raises(ValueError, match="intermediate"):
+        apply_bakron_block_update(ws, q, f_out, f_in, ws, **kw)
+    with pytest.raises(ValueError, match="intermediate"):
+        apply_bakron_block_update(big[0], q, f_out, f_in, big.view(-1)[100:100 + 64 * 96].view(64, 96), **kw)
+    with pytest.raises(ValueError, match="workspace"):
+        apply_bakron_block_update(ws, ws, f_out, f_in, torch.empty_like(ws), **kw)
+    apply_bakron_block_update(big[0], q, f_out, f_in, big[1], **kw)  # adjacent, not overlapping
     torch.cuda.synchronize()
 
 
