@@ -69,7 +69,7 @@ GEMM_HBM_BYTES = {"hessian_capture": 2.435e9, "ldlq_span_update": 1.485e8}
 HADAMARD_HBM_BYTES = {"left": 1.1782e8, "right": 1.1765e8}
 # Same counters for the BaKron top band's left + right launches (profiles/bakron_band_kernels_config4_gate.md):
 # mostly the right product's re-reads of the input factor.
-BAKRON_TOP_BAND_HBM_BYTES = 5.520e9
+BAKRON_TOP_BAND_HBM_BYTES = 5.515e9
 
 LAYER_EXPERTS = 384
 LAYER_TOKENS = 65536

@@ -19,7 +19,7 @@
 // last - o because the factors are block-lower, Lin(c, s) = 0 for s > c).  The sums run over s in
 // ascending order; each source block is one 16 x 16 x 16 product.
 //
-// Four waves per 256-thread workgroup, no LDS and no barriers; each wave computes kT target blocks (below),
+// Four waves per 256-thread workgroup, no LDS and no barriers; each wave computes a tile of target blocks (below),
 // and each (target, source) block product is four v_mfma_f32_16x16x4_f32.  The sixteen k of a block product
 // are split as k = 4 g + q over the instruction q = 0..3 and the lane's group g = lane / 16, so that a
 // lane's A operands for the four instructions are one float4 of a row (row lane % 16, columns 4 g .. 4 g + 3),
@@ -37,9 +37,10 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kB = 16;
 constexpr int kWaves = 4;
 
-// Target tile of a wave: kT blocks along the product's shared axis (rows o of the left product, columns c of
-// the right one) by kI columns (left) or kO rows (right); each block keeps its own accumulator.
-constexpr int kT = 4;
+// Target tile of a wave, each block with its own accumulator: kLRows row blocks by kLCols column blocks in the
+// left product, kRRows by kRCols in the right one.
+constexpr int kLRows = 8, kLCols = 1;
+constexpr int kRRows = 2, kRCols = 4;
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 
@@ -51,12 +52,12 @@ __device__ __forceinline__ f32x4 mfma4(float4 a, f32x4 b, f32x4 acc) {
     return acc;
 }
 
-// Left: wave w handles column blocks i0 .. i0 + kI - 1 (i0 = kI (w / chunks)) and rows o0 .. o0 + kT - 1 of the
+// Left: wave w handles column blocks i0 .. i0 + kLCols - 1 (i0 = kLCols (w / chunks)) and rows
+// o0 .. o0 + kLRows - 1 of the
 // union of those columns' targets [max(0, first - i), min(ob, last - i)), every (row, column) a target of its
 // own or skipped; a column's sources are the rows [max(0, first - i), min(ob, middle - i)), so a column takes
-// part in the source steps inside its range only (a wave-uniform branch).  Each Lout block loaded serves kI
-// columns and each error block kT rows.
-constexpr int kI = 2;
+// part in the source steps inside its range only (a wave-uniform branch).  Each Lout block loaded serves kLCols
+// columns and each error block kLRows rows.
 
 __global__ __launch_bounds__(kWaves * 64) void bakron_left_kernel(const float* __restrict__ T,
                                                                    const float* __restrict__ Q,
@@ -65,22 +66,22 @@ __global__ __launch_bounds__(kWaves * 64) void bakron_left_kernel(const float* _
                                                                    int first, int middle, int last,
                                                                    int64_t lout_stride) {
     const int ob = n_out / kB, ib = n_in / kB;
-    const int chunks = (min(ob, last - first + kI - 1) + kT - 1) / kT;
+    const int chunks = (min(ob, last - first + kLCols - 1) + kLRows - 1) / kLRows;
     const int lane = static_cast<int>(threadIdx.x) & 63;
     const int64_t slot = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
-    const int col_groups = (ib + kI - 1) / kI;
+    const int col_groups = (ib + kLCols - 1) / kLCols;
     if (slot >= static_cast<int64_t>(col_groups) * chunks) return;
-    const int i0 = kI * static_cast<int>(slot / chunks), chunk = static_cast<int>(slot % chunks);
-    const int i_last = min(ib, i0 + kI) - 1;
+    const int i0 = kLCols * static_cast<int>(slot / chunks), chunk = static_cast<int>(slot % chunks);
+    const int i_last = min(ib, i0 + kLCols) - 1;
     // union of the columns' target rows and sources
     const int o_lo = max(0, first - i_last), o_hi = min(ob, last - i0);
-    const int o0 = o_lo + kT * chunk;
+    const int o0 = o_lo + kLRows * chunk;
     if (o0 >= o_hi) return;
-    int sb[kI], se[kI];
-    bool col_ok[kI];
+    int sb[kLCols], se[kLCols];
+    bool col_ok[kLCols];
     int s_lo = ob, s_hi = 0;
 #pragma unroll
-    for (int u = 0; u < kI; ++u) {
+    for (int u = 0; u < kLCols; ++u) {
         const int i = i0 + u;
         col_ok[u] = i < ib;
         sb[u] = max(0, first - i);
@@ -98,63 +99,63 @@ __global__ __launch_bounds__(kWaves * 64) void bakron_left_kernel(const float* _
     const int c = lane & 15, g = lane >> 4;
     // lane's A rows: Lout rows 16 o + c for the tile's row blocks (a block past o_hi repeats the last one and is
     // not stored), columns 16 s + 4 g ..; B: rows 16 s + 4 g + q of columns 16 i + c
-    const float* a_row[kT];
+    const float* a_row[kLRows];
 #pragma unroll
-    for (int t = 0; t < kT; ++t)
+    for (int t = 0; t < kLRows; ++t)
         a_row[t] = Lout + static_cast<int64_t>(kB * min(o0 + t, o_hi - 1) + c) * n_out + 4 * g;
-    int64_t b_col[kI];
+    int64_t b_col[kLCols];
 #pragma unroll
-    for (int u = 0; u < kI; ++u) b_col[u] = static_cast<int64_t>(4 * g) * n_in + kB * min(i0 + u, ib - 1) + c;
-    f32x4 acc[kI][kT];
+    for (int u = 0; u < kLCols; ++u) b_col[u] = static_cast<int64_t>(4 * g) * n_in + kB * min(i0 + u, ib - 1) + c;
+    f32x4 acc[kLCols][kLRows];
 #pragma unroll
-    for (int u = 0; u < kI; ++u)
+    for (int u = 0; u < kLCols; ++u)
 #pragma unroll
-        for (int t = 0; t < kT; ++t) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float4 a_nx[kT] = {};
-    f32x4 b_nx[kI] = {};
+        for (int t = 0; t < kLRows; ++t) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float4 a_nx[kLRows] = {};
+    f32x4 b_nx[kLCols] = {};
     if (s_lo < s_hi) {
 #pragma unroll
-        for (int t = 0; t < kT; ++t) a_nx[t] = ld4(a_row[t] + kB * s_lo);
+        for (int t = 0; t < kLRows; ++t) a_nx[t] = ld4(a_row[t] + kB * s_lo);
 #pragma unroll
-        for (int u = 0; u < kI; ++u) {
+        for (int u = 0; u < kLCols; ++u) {
             const int64_t off = static_cast<int64_t>(kB * s_lo) * n_in + b_col[u];
 #pragma unroll
             for (int q = 0; q < 4; ++q) b_nx[u][q] = Q[off + q * n_in] - T[off + q * n_in];
         }
     }
     for (int s = s_lo; s < s_hi; ++s) {
-        float4 a[kT];
-        f32x4 b[kI];
+        float4 a[kLRows];
+        f32x4 b[kLCols];
 #pragma unroll
-        for (int t = 0; t < kT; ++t) a[t] = a_nx[t];
+        for (int t = 0; t < kLRows; ++t) a[t] = a_nx[t];
 #pragma unroll
-        for (int u = 0; u < kI; ++u) b[u] = b_nx[u];
+        for (int u = 0; u < kLCols; ++u) b[u] = b_nx[u];
         if (s + 1 < s_hi) {
 #pragma unroll
-            for (int t = 0; t < kT; ++t) a_nx[t] = ld4(a_row[t] + kB * (s + 1));
+            for (int t = 0; t < kLRows; ++t) a_nx[t] = ld4(a_row[t] + kB * (s + 1));
 #pragma unroll
-            for (int u = 0; u < kI; ++u) {
+            for (int u = 0; u < kLCols; ++u) {
                 const int64_t off = static_cast<int64_t>(kB * (s + 1)) * n_in + b_col[u];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) b_nx[u][q] = Q[off + q * n_in] - T[off + q * n_in];
             }
         }
 #pragma unroll
-        for (int u = 0; u < kI; ++u) {
+        for (int u = 0; u < kLCols; ++u) {
             if (s < sb[u] || s >= se[u]) continue;  // uniform: the column's own source range
 #pragma unroll
-            for (int t = 0; t < kT; ++t) acc[u][t] = mfma4(a[t], b[u], acc[u][t]);
+            for (int t = 0; t < kLRows; ++t) acc[u][t] = mfma4(a[t], b[u], acc[u][t]);
         }
     }
     // acc[u][t][r] = I(o0 + t, i0 + u)[4 g + r][c]; every target of the tile is written, zero when its column
     // has no sources
 #pragma unroll
-    for (int u = 0; u < kI; ++u) {
+    for (int u = 0; u < kLCols; ++u) {
         const int i = i0 + u;
         if (!col_ok[u]) continue;
         const int ob_lo = max(0, first - i), ob_hi = min(ob, last - i);
 #pragma unroll
-        for (int t = 0; t < kT; ++t) {
+        for (int t = 0; t < kLRows; ++t) {
             const int o = o0 + t;
             if (o < ob_lo || o >= ob_hi) continue;
             float* out = I + static_cast<int64_t>(kB * o + 4 * g) * n_in + kB * i + c;
@@ -164,12 +165,12 @@ __global__ __launch_bounds__(kWaves * 64) void bakron_left_kernel(const float* _
     }
 }
 
-// Right: wave w handles row blocks o0 .. o0 + kO - 1 (o0 = kO (w / chunks)) and columns c0 .. c0 + kT - 1 of the
+// Right: wave w handles row blocks o0 .. o0 + kRRows - 1 (o0 = kRRows (w / chunks)) and columns
+// c0 .. c0 + kRCols - 1 of the
 // union of those rows' targets [max(0, middle - o), min(ib, last - o)), every (row, column) a target of its own
 // or skipped; a row's sources are [max(0, first - o), min(ib, middle, last - o)), so a row takes part in the
-// source steps inside its range only (a wave-uniform branch).  Each Lin block loaded serves kO rows and each
-// I block kT columns.
-constexpr int kO = 2;
+// source steps inside its range only (a wave-uniform branch).  Each Lin block loaded serves kRRows rows and each
+// I block kRCols columns.
 
 __global__ __launch_bounds__(kWaves * 64) void bakron_right_kernel(float* __restrict__ T,
                                                                     const float* __restrict__ Lin,
@@ -177,22 +178,22 @@ __global__ __launch_bounds__(kWaves * 64) void bakron_right_kernel(float* __rest
                                                                     int n_in, int first, int middle, int last,
                                                                     int64_t lin_stride) {
     const int ob = n_out / kB, ib = n_in / kB;
-    const int chunks = (min(ib, last - middle + kO - 1) + kT - 1) / kT;
+    const int chunks = (min(ib, last - middle + kRRows - 1) + kRCols - 1) / kRCols;
     const int lane = static_cast<int>(threadIdx.x) & 63;
     const int64_t slot = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
-    const int row_groups = (ob + kO - 1) / kO;
+    const int row_groups = (ob + kRRows - 1) / kRRows;
     if (slot >= static_cast<int64_t>(row_groups) * chunks) return;
-    const int o0 = kO * static_cast<int>(slot / chunks), chunk = static_cast<int>(slot % chunks);
-    const int o_last = min(ob, o0 + kO) - 1;
+    const int o0 = kRRows * static_cast<int>(slot / chunks), chunk = static_cast<int>(slot % chunks);
+    const int o_last = min(ob, o0 + kRRows) - 1;
     // union of the rows' target columns and sources
     const int c_lo = max(0, middle - o_last), c_hi = min(ib, last - o0);
-    const int c0 = c_lo + kT * chunk;
+    const int c0 = c_lo + kRCols * chunk;
     if (c0 >= c_hi) return;
-    int sb[kO], se[kO];
-    bool row_ok[kO];
+    int sb[kRRows], se[kRRows];
+    bool row_ok[kRRows];
     int s_lo = ib, s_hi = 0;
 #pragma unroll
-    for (int a = 0; a < kO; ++a) {
+    for (int a = 0; a < kRRows; ++a) {
         const int o = o0 + a;
         row_ok[a] = o < ob;
         sb[a] = max(0, first - o);
@@ -210,49 +211,49 @@ __global__ __launch_bounds__(kWaves * 64) void bakron_right_kernel(float* __rest
     const int c = lane & 15, g = lane >> 4;
     // lane's A rows: I rows 16 o + c; B rows: Lin rows 16 cb + c for the tile's column blocks cb (a block past
     // c_hi repeats the last one and is not stored); columns 16 s + 4 g ..
-    const float* a_row[kO];
+    const float* a_row[kRRows];
 #pragma unroll
-    for (int a = 0; a < kO; ++a) a_row[a] = I + static_cast<int64_t>(kB * min(o0 + a, ob - 1) + c) * n_in + 4 * g;
-    const float* b_row[kT];
+    for (int a = 0; a < kRRows; ++a) a_row[a] = I + static_cast<int64_t>(kB * min(o0 + a, ob - 1) + c) * n_in + 4 * g;
+    const float* b_row[kRCols];
 #pragma unroll
-    for (int t = 0; t < kT; ++t)
+    for (int t = 0; t < kRCols; ++t)
         b_row[t] = Lin + static_cast<int64_t>(kB * min(c0 + t, c_hi - 1) + c) * n_in + 4 * g;
-    f32x4 acc[kO][kT];
+    f32x4 acc[kRRows][kRCols];
 #pragma unroll
-    for (int a = 0; a < kO; ++a)
+    for (int a = 0; a < kRRows; ++a)
 #pragma unroll
-        for (int t = 0; t < kT; ++t) acc[a][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float4 a_nx[kO], b_nx[kT];
+        for (int t = 0; t < kRCols; ++t) acc[a][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float4 a_nx[kRRows], b_nx[kRCols];
 #pragma unroll
-    for (int a = 0; a < kO; ++a) a_nx[a] = ld4(a_row[a] + kB * s_lo);
+    for (int a = 0; a < kRRows; ++a) a_nx[a] = ld4(a_row[a] + kB * s_lo);
 #pragma unroll
-    for (int t = 0; t < kT; ++t) b_nx[t] = ld4(b_row[t] + kB * s_lo);
+    for (int t = 0; t < kRCols; ++t) b_nx[t] = ld4(b_row[t] + kB * s_lo);
     for (int s = s_lo; s < s_hi; ++s) {
-        float4 av[kO], b[kT];
+        float4 av[kRRows], b[kRCols];
 #pragma unroll
-        for (int a = 0; a < kO; ++a) av[a] = a_nx[a];
+        for (int a = 0; a < kRRows; ++a) av[a] = a_nx[a];
 #pragma unroll
-        for (int t = 0; t < kT; ++t) b[t] = b_nx[t];
+        for (int t = 0; t < kRCols; ++t) b[t] = b_nx[t];
         if (s + 1 < s_hi) {
 #pragma unroll
-            for (int a = 0; a < kO; ++a) a_nx[a] = ld4(a_row[a] + kB * (s + 1));
+            for (int a = 0; a < kRRows; ++a) a_nx[a] = ld4(a_row[a] + kB * (s + 1));
 #pragma unroll
-            for (int t = 0; t < kT; ++t) b_nx[t] = ld4(b_row[t] + kB * (s + 1));
+            for (int t = 0; t < kRCols; ++t) b_nx[t] = ld4(b_row[t] + kB * (s + 1));
         }
 #pragma unroll
-        for (int a = 0; a < kO; ++a) {
+        for (int a = 0; a < kRRows; ++a) {
             if (s < sb[a] || s >= se[a]) continue;  // uniform: the row's own source range
 #pragma unroll
-            for (int t = 0; t < kT; ++t) acc[a][t] = mfma4(av[a], f32x4{b[t].x, b[t].y, b[t].z, b[t].w}, acc[a][t]);
+            for (int t = 0; t < kRCols; ++t) acc[a][t] = mfma4(av[a], f32x4{b[t].x, b[t].y, b[t].z, b[t].w}, acc[a][t]);
         }
     }
 #pragma unroll
-    for (int a = 0; a < kO; ++a) {
+    for (int a = 0; a < kRRows; ++a) {
         const int o = o0 + a;
         if (!row_ok[a] || sb[a] >= se[a]) continue;
         const int ce = min(ib, last - o), cb = max(0, middle - o);
 #pragma unroll
-        for (int t = 0; t < kT; ++t) {
+        for (int t = 0; t < kRCols; ++t) {
             const int col = c0 + t;
             if (col < cb || col >= ce) continue;
             float* out = T + static_cast<int64_t>(kB * o + 4 * g) * n_in + kB * col + c;
@@ -288,12 +289,12 @@ int qsrt_bakron_band_update_f32(float* workspace, const float* quantized, const 
           last_diagonal <= diagonals))
         return qsrt::fail(qsrt::kBadArgument, "diagonals must satisfy 0 <= first < middle < last <= %lld",
                           static_cast<long long>(diagonals));
-    const int64_t left_span_union = ob < last_diagonal - first_diagonal + kI - 1 ? ob
-                                                                                 : last_diagonal - first_diagonal + kI - 1;
-    const int64_t left_waves = ((ib + kI - 1) / kI) * ((left_span_union + kT - 1) / kT);
-    const int64_t right_span_union = ib < last_diagonal - middle_diagonal + kO - 1 ? ib
-                                                                                   : last_diagonal - middle_diagonal + kO - 1;
-    const int64_t right_waves = ((ob + kO - 1) / kO) * ((right_span_union + kT - 1) / kT);
+    const int64_t left_span_union = ob < last_diagonal - first_diagonal + kLCols - 1 ? ob
+                                                                                 : last_diagonal - first_diagonal + kLCols - 1;
+    const int64_t left_waves = ((ib + kLCols - 1) / kLCols) * ((left_span_union + kLRows - 1) / kLRows);
+    const int64_t right_span_union = ib < last_diagonal - middle_diagonal + kRRows - 1 ? ib
+                                                                                   : last_diagonal - middle_diagonal + kRRows - 1;
+    const int64_t right_waves = ((ob + kRRows - 1) / kRRows) * ((right_span_union + kRCols - 1) / kRCols);
     const dim3 block(kWaves * 64);
     hipLaunchKernelGGL(bakron_left_kernel, dim3(static_cast<unsigned>((left_waves + kWaves - 1) / kWaves),
                                                 static_cast<unsigned>(batch)),
