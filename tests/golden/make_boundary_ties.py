@@ -2,7 +2,7 @@
 boundary state than the CPU oracle (``oracle/viterbi_ref.c``) on the same
 BlockLDLQ target.  Runs on a GPU box:
 
-    python tests/golden/make_boundary_ties.py --out gpurun_out/boundary_ties_k3.npz
+    python tests/golden/make_boundary_ties.py --out /tmp/boundary_ties_k3.npz
 
 It encodes the config-3 strip of ``tests/test_e2e_parity_gpu.py`` with
 ``quantize_qsrt`` at global scales a few float32 steps from the searched one
