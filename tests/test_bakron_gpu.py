@@ -4,10 +4,13 @@ float64 oracle (oracle/bakron.py).
 
 Bar: FP32 on the matrix cores, so every element of the updated targets and
 of the intermediate is within 1e-5 of the float64 value relative to the same
-sums taken over absolute values (|Lout| |Q - T| |Lin|^T), plus 1e-7.
+sums taken over absolute values (|Lout| |Q - T| |Lin|^T), plus one FP32 ulp
+of the result (the kernel stores T + update rounded to FP32) and 1e-7.
 Blocks outside the bands must be untouched bit for bit; the intermediate is
 pre-filled with NaN, so a read of a block the call did not write shows up.
-The encoders: a lockstep batch equals independent encodes bit for bit, and a
+At the full config-4 gate shape the reference is the dense masked product in
+float64 on the device.  The encoders: a lockstep batch equals independent
+encodes bit for bit, and a
 shared rank-2 factor equals the same factor expanded per member (the
 reference's tests/test_two_sided_rounding.py:244-326)."""
 
@@ -30,6 +33,7 @@ DEV = torch.device("cuda:0")
 B = 16
 REL = 1e-5
 ABS = 1e-7
+ULP = 2.0 ** -23  # one FP32 ulp relative to the value
 
 
 def _say(msg):
@@ -84,8 +88,8 @@ def _check(T, Q, lo, li, first, middle, last):
         assert np.all(np.isfinite(got_i[j][band_i])) and np.all(np.isfinite(got_t[j]))
         err_t = np.abs(got_t[j][band_t] - want_t[j][band_t])
         err_i = np.abs(got_i[j][band_i] - want_i[j][band_i])
-        assert np.all(err_t <= REL * abs_t[j][band_t] + ABS), float(err_t.max())
-        assert np.all(err_i <= REL * abs_i[j][band_i] + ABS), float(err_i.max())
+        assert np.all(err_t <= REL * abs_t[j][band_t] + ULP * np.abs(want_t[j][band_t]) + ABS), float(err_t.max())
+        assert np.all(err_i <= REL * abs_i[j][band_i] + ULP * np.abs(want_i[j][band_i]) + ABS), float(err_i.max())
         worst = max(worst, float((err_t / (abs_t[j][band_t] + 1e-30)).max()))
     return worst
 
@@ -215,3 +219,49 @@ def test_hip_updates_choose_the_float64_path():
     differ = float((hip.payload.cpu().long() != ref.payload.long()).double().mean())
     _say(f"[bakron]   payload elements differing from the float64 encode: {differ:.2e}")
     assert differ <= 1e-3
+
+
+def _band_mask_t(ob, ib, first, last):
+    o = torch.arange(ob, device=DEV)[:, None]
+    i = torch.arange(ib, device=DEV)[None, :]
+    m = ((o + i) >= first) & ((o + i) < last)
+    return m.repeat_interleave(B, 0).repeat_interleave(B, 1)
+
+
+@pytest.mark.parametrize("first,middle,last", [(0, 287, 575), (143, 215, 287), (500, 501, 575)])
+def test_config4_gate_bands_match_the_dense_float64_product(first, middle, last):
+    """Full config-4 gate shape (2048 x 7168 in the encoder orientation): the
+    kernel against T + M2 (Lout (M1 (Q - T)) Lin^T) in float64 on the device,
+    the dense form the CPU tests pin to the block oracle for block-lower
+    factors; same bar as above."""
+
+    n_out, n_in = 2048, 7168
+    ob, ib = n_out // B, n_in // B
+    _say(f"[bakron] config-4 gate {n_out}x{n_in} band [{first},{middle},{last})")
+    g = torch.Generator(device=DEV).manual_seed(9000 + first)
+    T = torch.randn((n_out, n_in), device=DEV, generator=g)
+    Q = torch.round(T * 4) / 4 + 0.01 * torch.randn((n_out, n_in), device=DEV, generator=g)
+    lo = torch.randn((n_out, n_out), device=DEV, generator=g) / n_out ** 0.5
+    li = torch.randn((n_in, n_in), device=DEV, generator=g) / n_in ** 0.5
+    lo *= torch.kron(torch.tril(torch.ones(ob, ob, device=DEV)), torch.ones(B, B, device=DEV))
+    li *= torch.kron(torch.tril(torch.ones(ib, ib, device=DEV)), torch.ones(B, B, device=DEV))
+    ws = T.clone()
+    inter = torch.full_like(T, float("nan"))
+    apply_bakron_block_update(ws, Q, lo, li, inter, first_diagonal=first, middle_diagonal=middle,
+                              last_diagonal=last, block_size=B)
+    torch.cuda.synchronize()
+    m1 = _band_mask_t(ob, ib, first, middle)
+    m2 = _band_mask_t(ob, ib, middle, last)
+    mi = _band_mask_t(ob, ib, first, last)
+    delta = torch.where(m1, (Q - T).double(), 0.0)
+    left = lo.double() @ delta
+    want = T.double() + torch.where(m2, left @ li.double().t().contiguous(), 0.0)
+    abs_left = lo.double().abs() @ delta.abs()
+    abs_upd = abs_left @ li.double().abs().t().contiguous()
+    assert torch.equal(ws[~m2], T[~m2]), "targets outside the next band changed"
+    assert bool(torch.isnan(inter[~mi]).all()), "intermediate written outside [first, last)"
+    err_t = (ws.double() - want).abs()[m2]
+    err_i = (inter.double() - left).abs()[mi]
+    assert bool((err_t <= REL * abs_upd[m2] + ULP * want[m2].abs() + ABS).all()), float(err_t.max())
+    assert bool((err_i <= REL * abs_left[mi] + ULP * left[mi].abs() + ABS).all()), float(err_i.max())
+    _say(f"[bakron]   worst error / |terms| {float((err_t / (abs_upd[m2] + 1e-30)).max()):.2e}")
