@@ -885,15 +885,18 @@ def hadamard_bench(steps: int = 5):
     return {"workload": f"[{k} x {n}] f32, block 128, fused signs, in place", **out}
 
 
-def _bakron_band_flops(ob: int, ib: int, first: int, middle: int, last: int) -> int:
+def _bakron_band_flops(ob: int, ib: int, first: int, middle: int, last: int, block_lower: bool = False) -> int:
     """Algorithmic flops of one fused band update: 2 * 16^3 per (target block,
-    source block) pair of the left and right products."""
+    source block) pair of the left and right products (with ``block_lower``,
+    the left pairs whose output-factor block is not a zero block above the
+    diagonal)."""
 
     pairs = 0
     for d in range(first, last):
         for o in range(max(0, d - ib + 1), min(ob, d + 1)):
             i = d - o
-            pairs += max(0, min(ob, middle - i) - max(0, first - i))
+            s_end = min(ob, middle - i, o + 1) if block_lower else min(ob, middle - i)
+            pairs += max(0, s_end - max(0, first - i))
             if d >= middle:
                 pairs += max(0, min(ib, middle, last - o) - max(0, first - o))
     return 2 * 16 ** 3 * pairs
@@ -943,6 +946,13 @@ def bakron_bench(steps: int = 5):
     top_flops = _bakron_band_flops(ob, ib, *top)
     achieved = top_flops / (top_ms / 1e3) / 1e12
 
+    def hip_lower(band):
+        apply_bakron_block_update(T, Q, l_out, l_in, inter, first_diagonal=band[0], middle_diagonal=band[1],
+                                  last_diagonal=band[2], block_size=16, block_lower=True)
+
+    lower_ms = _time_ms(lambda: hip_lower(top), steps)
+    lower_flops = _bakron_band_flops(ob, ib, *top, block_lower=True)
+
     def all_hip():
         for band in bands:
             hip(band)
@@ -962,7 +972,10 @@ def bakron_bench(steps: int = 5):
             "top_band": {"diagonals": list(top), "ms": round(top_ms, 4), "roofline": {
                 "bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "traffic": round(BAKRON_TOP_BAND_HBM_BYTES),
-                "algorithmic": f"2 x 16^3 flops per (target, source) block pair x {top_flops // 8192} pairs"}},
+                "algorithmic": f"2 x 16^3 flops per (target, source) block pair x {top_flops // 8192} pairs"},
+                "block_lower": {"ms": round(lower_ms, 4),
+                                "tflops": round(lower_flops / (lower_ms / 1e3) / 1e12, 2),
+                                "pairs": lower_flops // 8192}},
             "recursion": {"bands": len(bands), "hip_ms": round(all_ms, 3), "torch_bounding_box_ms": round(torch_ms, 3),
                           "hip_tflops": round(all_flops / (all_ms / 1e3) / 1e12, 2)}}
 

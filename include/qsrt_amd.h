@@ -291,6 +291,21 @@ int qsrt_bakron_band_update_f32(float *workspace, const float *quantized, const 
                                 void *stream);
 
 /*
+ * qsrt_bakron_band_update_f32 for block-lower output factors (Lout(o, s) = 0
+ * for every block s > o, as the unit-block-lower factors of the BaKron
+ * recurrence are): the left product skips those blocks.  For such factors
+ * and finite inputs the result equals qsrt_bakron_band_update_f32's (up to
+ * the sign of a zero).  No counterpart in the reference, whose launcher
+ * (qsrt/csrc/sqg_quantize.cu:991-1100) always takes the full ranges; for
+ * callers whose factors are block-lower by construction.
+ */
+int qsrt_bakron_band_update_lower_f32(float *workspace, const float *quantized, const float *output_factor,
+                                      const float *input_factor, float *intermediate, int64_t batch, int64_t n_out,
+                                      int64_t n_in, int64_t output_factor_batch_stride,
+                                      int64_t input_factor_batch_stride, int64_t first_diagonal,
+                                      int64_t middle_diagonal, int64_t last_diagonal, void *stream);
+
+/*
  * BlockLDLQ step, batched over B members (member m quantizes source
  * src[m]).  For the 16-row block [blk, blk + 16) of a span ending at row
  * `end`, every member's target

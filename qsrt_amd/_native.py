@@ -73,6 +73,10 @@ SIGNATURES: dict[str, tuple] = {
         _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                  _c_i64, _c_i64, _c_i64, _c_void_p],
     ),
+    "qsrt_bakron_band_update_lower_f32": (
+        _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                 _c_i64, _c_i64, _c_i64, _c_void_p],
+    ),
     "qsrt_ldlq_targets": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64,

@@ -64,7 +64,7 @@ __global__ __launch_bounds__(kWaves * 64) void bakron_left_kernel(const float* _
                                                                    const float* __restrict__ Lout,
                                                                    float* __restrict__ I, int n_out, int n_in,
                                                                    int first, int middle, int last,
-                                                                   int64_t lout_stride) {
+                                                                   int64_t lout_stride, int lower) {
     const int ob = n_out / kB, ib = n_in / kB;
     const int chunks = (min(ob, last - first + kLCols - 1) + kLRows - 1) / kLRows;
     const int lane = static_cast<int>(threadIdx.x) & 63;
@@ -91,6 +91,8 @@ __global__ __launch_bounds__(kWaves * 64) void bakron_left_kernel(const float* _
             s_hi = max(s_hi, se[u]);
         }
     }
+    // a block-lower Lout has Lout(o, s) = 0 for s > o: the tile's rows need no source past its last row
+    if (lower) s_hi = min(s_hi, min(o0 + kLRows, o_hi));
     const int64_t mat = static_cast<int64_t>(n_out) * n_in;
     T += blockIdx.y * mat;
     Q += blockIdx.y * mat;
@@ -144,7 +146,10 @@ __global__ __launch_bounds__(kWaves * 64) void bakron_left_kernel(const float* _
         for (int u = 0; u < kLCols; ++u) {
             if (s < sb[u] || s >= se[u]) continue;  // uniform: the column's own source range
 #pragma unroll
-            for (int t = 0; t < kLRows; ++t) acc[u][t] = mfma4(a[t], b[u], acc[u][t]);
+            for (int t = 0; t < kLRows; ++t) {
+                if (lower && s > o0 + t) continue;  // uniform: a zero block of a block-lower Lout
+                acc[u][t] = mfma4(a[t], b[u], acc[u][t]);
+            }
         }
     }
     // acc[u][t][r] = I(o0 + t, i0 + u)[4 g + r][c]; every target of the tile is written, zero when its column
@@ -267,11 +272,10 @@ __global__ __launch_bounds__(kWaves * 64) void bakron_right_kernel(float* __rest
 
 extern "C" {
 
-int qsrt_bakron_band_update_f32(float* workspace, const float* quantized, const float* output_factor,
-                                const float* input_factor, float* intermediate, int64_t batch, int64_t n_out,
-                                int64_t n_in, int64_t output_factor_batch_stride, int64_t input_factor_batch_stride,
-                                int64_t first_diagonal, int64_t middle_diagonal, int64_t last_diagonal,
-                                void* stream_handle) {
+static int band_update(float* workspace, const float* quantized, const float* output_factor,
+                       const float* input_factor, float* intermediate, int64_t batch, int64_t n_out, int64_t n_in,
+                       int64_t output_factor_batch_stride, int64_t input_factor_batch_stride, int64_t first_diagonal,
+                       int64_t middle_diagonal, int64_t last_diagonal, void* stream_handle, int lower) {
     hipStream_t stream = static_cast<hipStream_t>(stream_handle);
     if (!workspace || !quantized || !output_factor || !input_factor || !intermediate)
         return qsrt::fail(qsrt::kBadArgument, "null pointer argument");
@@ -300,7 +304,7 @@ int qsrt_bakron_band_update_f32(float* workspace, const float* quantized, const 
                                                 static_cast<unsigned>(batch)),
                        block, 0, stream, workspace, quantized, output_factor, intermediate, static_cast<int>(n_out),
                        static_cast<int>(n_in), static_cast<int>(first_diagonal), static_cast<int>(middle_diagonal),
-                       static_cast<int>(last_diagonal), output_factor_batch_stride);
+                       static_cast<int>(last_diagonal), output_factor_batch_stride, lower);
     QSRT_HIP_TRY(hipGetLastError());
     hipLaunchKernelGGL(bakron_right_kernel, dim3(static_cast<unsigned>((right_waves + kWaves - 1) / kWaves),
                                                  static_cast<unsigned>(batch)),
@@ -309,6 +313,26 @@ int qsrt_bakron_band_update_f32(float* workspace, const float* quantized, const 
                        static_cast<int>(last_diagonal), input_factor_batch_stride);
     QSRT_HIP_TRY(hipGetLastError());
     return qsrt::kOk;
+}
+
+int qsrt_bakron_band_update_f32(float* workspace, const float* quantized, const float* output_factor,
+                                const float* input_factor, float* intermediate, int64_t batch, int64_t n_out,
+                                int64_t n_in, int64_t output_factor_batch_stride, int64_t input_factor_batch_stride,
+                                int64_t first_diagonal, int64_t middle_diagonal, int64_t last_diagonal,
+                                void* stream_handle) {
+    return band_update(workspace, quantized, output_factor, input_factor, intermediate, batch, n_out, n_in,
+                       output_factor_batch_stride, input_factor_batch_stride, first_diagonal, middle_diagonal,
+                       last_diagonal, stream_handle, 0);
+}
+
+int qsrt_bakron_band_update_lower_f32(float* workspace, const float* quantized, const float* output_factor,
+                                      const float* input_factor, float* intermediate, int64_t batch, int64_t n_out,
+                                      int64_t n_in, int64_t output_factor_batch_stride,
+                                      int64_t input_factor_batch_stride, int64_t first_diagonal,
+                                      int64_t middle_diagonal, int64_t last_diagonal, void* stream_handle) {
+    return band_update(workspace, quantized, output_factor, input_factor, intermediate, batch, n_out, n_in,
+                       output_factor_batch_stride, input_factor_batch_stride, first_diagonal, middle_diagonal,
+                       last_diagonal, stream_handle, 1);
 }
 
 }  // extern "C"

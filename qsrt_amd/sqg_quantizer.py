@@ -259,7 +259,8 @@ def _overlap(a: torch.Tensor, b: torch.Tensor) -> bool:
 
 def apply_bakron_block_update(workspace: torch.Tensor, quantized: torch.Tensor, output_factor: torch.Tensor,
                               input_factor: torch.Tensor, intermediate: torch.Tensor, *, first_diagonal: int,
-                              middle_diagonal: int, last_diagonal: int, block_size: int) -> None:
+                              middle_diagonal: int, last_diagonal: int, block_size: int,
+                              block_lower: bool = False) -> None:
     """One fused FP32 band propagation of the recursive BaKron rounding on the
     GPU (reference ``qsrt/sqg_quantizer.py:383-407`` over
     ``qsrt/csrc/sqg_quantize.cu:991-1100``): the intermediate receives
@@ -267,7 +268,10 @@ def apply_bakron_block_update(workspace: torch.Tensor, quantized: torch.Tensor, 
     diagonals [first, last), and the workspace gains
     ``intermediate Lin^T`` on the next band [middle, last).  Runs the HIP
     kernel behind ``qsrt_bakron_band_update_f32`` on the current stream; the
-    checks and their messages follow the reference launcher's."""
+    checks and their messages follow the reference launcher's.
+    ``block_lower=True`` (not in the reference) promises a block-lower output
+    factor and runs ``qsrt_bakron_band_update_lower_f32``, which skips its
+    zero blocks; the result is the same for such factors."""
 
     if not workspace.is_cuda:
         raise ValueError("workspace must be CUDA")
@@ -312,7 +316,8 @@ def apply_bakron_block_update(workspace: torch.Tensor, quantized: torch.Tensor, 
         raise ValueError("invalid recursive BaKron diagonal range")
     lib = _native.lib()
     with torch.cuda.device(workspace.device):
-        _native.check(lib.qsrt_bakron_band_update_f32(
+        fn = lib.qsrt_bakron_band_update_lower_f32 if block_lower else lib.qsrt_bakron_band_update_f32
+        _native.check(fn(
             workspace.data_ptr(), quantized.data_ptr(), output_factor.data_ptr(), input_factor.data_ptr(),
             intermediate.data_ptr(), batch, n_out, n_in, 0 if output_factor.ndim == 2 else n_out * n_out,
             0 if input_factor.ndim == 2 else n_in * n_in, first, middle, last,

@@ -18,7 +18,8 @@ quantizer keeps one legal path per tile.  Three equivalent recurrences:
 On the GPU in FP32 with 16 x 16 blocks, every band propagation of the
 divide and conquer (and of the lockstep batches) is the fused HIP band
 kernel (``qsrt_amd.sqg_quantizer.apply_bakron_block_update``, two launches
-per band, one wave per target block on the FP32 matrix cores); otherwise,
+per band on the FP32 matrix cores; with the factors computed here, which are
+unit-block-lower, the left launch skips their zero blocks); otherwise,
 and for the anti-diagonal recurrence, the update is two dense tensor
 products on the bands' bounding boxes.
 """
@@ -285,7 +286,7 @@ class _BakronState:
     one or a batch of matrices."""
 
     def __init__(self, weights, input_factor, output_factor, input_reverse, output_reverse, block_size, work_dtype,
-                 hip_update=False):
+                 hip_update=False, own_factors=True):
         self.b = block_size
         self.batched = weights.ndim == 3
         w = weights if self.batched else weights.unsqueeze(0)
@@ -299,6 +300,8 @@ class _BakronState:
         self.payload = None
         self.dtype = work_dtype
         self.intermediate = torch.empty_like(self.workspace) if hip_update else None
+        # factors computed here are unit-block-lower; supplied ones are taken as they come
+        self.block_lower = own_factors
 
     def propagate(self, first: int, middle: int, last: int) -> None:
         """Band [first, middle) into [middle, last): the fused HIP kernel when
@@ -309,7 +312,7 @@ class _BakronState:
             l_in = self.l_in[0] if self.l_in.ndim == 3 and self.l_in.shape[0] == 1 else self.l_in
             _hip_apply_update(self.workspace, self.quantized, l_out.contiguous(), l_in.contiguous(),
                               self.intermediate, first_diagonal=first, middle_diagonal=middle,
-                              last_diagonal=last, block_size=self.b)
+                              last_diagonal=last, block_size=self.b, block_lower=self.block_lower)
         else:
             _propagate_band(self.workspace, self.quantized, self.l_out, self.l_in, first=first, middle=middle,
                             last=last, block_size=self.b)
@@ -467,7 +470,7 @@ def bakron_block_round_encoder_prepared_batch(weights: torch.Tensor, input_facto
         if tuple(reverse.shape) != (dim,) or reverse.device != weights.device or reverse.dtype != torch.long:
             raise ValueError(f"{name} has incompatible geometry")
     st = _BakronState(weights, input_factors, output_factors, input_reverse, output_reverse, block_size, work_dtype,
-                      hip_update=True)
+                      hip_update=True, own_factors=False)
     _recurse(st, quantize_tiles, 0, st.ob + st.ib - 1)
     return st.result(weights.dtype)
 

@@ -61,18 +61,21 @@ def _inputs(batch, n_out, n_in, seed, shared):
     return T, Q, lo, li
 
 
-def _run(T, Q, lo, li, first, middle, last):
+def _run(T, Q, lo, li, first, middle, last, block_lower=False):
     ws = torch.from_numpy(T.copy()).to(DEV)
     inter = torch.full(T.shape, float("nan"), dtype=torch.float32, device=DEV)
     apply_bakron_block_update(ws, torch.from_numpy(Q).to(DEV), torch.from_numpy(lo).to(DEV),
                               torch.from_numpy(li).to(DEV), inter, first_diagonal=first, middle_diagonal=middle,
-                              last_diagonal=last, block_size=B)
+                              last_diagonal=last, block_size=B, block_lower=block_lower)
     torch.cuda.synchronize()
     return ws.cpu().numpy(), inter.cpu().numpy()
 
 
 def _check(T, Q, lo, li, first, middle, last):
     got_t, got_i = _run(T, Q, lo, li, first, middle, last)
+    # the block-lower entry point skips the zero blocks of these factors: the same values (== also equates -0, 0)
+    low_t, low_i = _run(T, Q, lo, li, first, middle, last, block_lower=True)
+    assert np.array_equal(low_t, got_t) and np.array_equal(low_i, got_i, equal_nan=True)
     T64, Q64 = T.astype(np.float64), Q.astype(np.float64)
     want_t, want_i = bk.band_update_batch(T64, Q64, lo.astype(np.float64), li.astype(np.float64), first, middle,
                                           last)
@@ -249,7 +252,11 @@ def test_config4_gate_bands_match_the_dense_float64_product(first, middle, last)
     inter = torch.full_like(T, float("nan"))
     apply_bakron_block_update(ws, Q, lo, li, inter, first_diagonal=first, middle_diagonal=middle,
                               last_diagonal=last, block_size=B)
+    ws_low, inter_low = T.clone(), torch.full_like(T, float("nan"))
+    apply_bakron_block_update(ws_low, Q, lo, li, inter_low, first_diagonal=first, middle_diagonal=middle,
+                              last_diagonal=last, block_size=B, block_lower=True)
     torch.cuda.synchronize()
+    assert torch.equal(ws_low, ws) and torch.equal(inter_low.nan_to_num(7.0), inter.nan_to_num(7.0))
     m1 = _band_mask_t(ob, ib, first, middle)
     m2 = _band_mask_t(ob, ib, middle, last)
     mi = _band_mask_t(ob, ib, first, last)
