@@ -263,12 +263,12 @@ class ExpertEncoder:
                 hs.append(shared)
                 qas.append([self.quant_args(name)])
             del p["h13"]
-        up = be.quantize_qsrt_batch(weights, hs, qas)  # regularises every weight in place
+        up = be.quantize_qsrt_batch(weights, hs, qas)
         kept = {}
-        for i, src in enumerate(sources):
+        for i, src in enumerate(sources):  # the float64 regularised weight and factor the recursion read
             if src["expert"] in keep_states:
-                kept[(i, "w1")] = (weights[2 * i], hs[2 * i]["L"])
-                kept[(i, "w3")] = (weights[2 * i + 1], hs[2 * i + 1]["L"])
+                kept[(i, "w1")] = (up[2 * i][0]["weight_r"], hs[2 * i]["L"])
+                kept[(i, "w3")] = (up[2 * i + 1][0]["weight_r"], hs[2 * i + 1]["L"])
         del weights, hs
         weights, hs, qas_d = [], [], []
         for i, p in enumerate(prepared):
@@ -286,7 +286,7 @@ class ExpertEncoder:
         down = be.quantize_qsrt_batch(weights, hs, qas_d, return_weight_q=False)
         for i, src in enumerate(sources):
             if src["expert"] in keep_states:
-                kept[(i, "w2")] = (weights[i], hs[i]["L"])
+                kept[(i, "w2")] = (down[i][0]["weight_r"], hs[i]["L"])
         del weights, hs
         out = []
         for i, src in enumerate(sources):

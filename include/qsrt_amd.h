@@ -130,6 +130,18 @@ int qsrt_hadamard(float *x, int64_t rows, int64_t cols, int64_t ld, int block, i
                   const float *pre_div, const float *post_mul, void *stream);
 
 /*
+ * qsrt_hadamard on a float64 matrix with float64 vectors (x 16-byte
+ * aligned, cols and ld multiples of 4).  The encoder's regularisation
+ * rotates in float64 (W / sv, then H; W / su, then H on the other side) so
+ * that the weight the BlockLDLQ recursion reads is rounded to FP32 only in
+ * the tile targets.  Replaces the same reference functions as qsrt_hadamard
+ * on the regularize path (qsrt/exl3_encoder_backend.py:2580-2708, which
+ * rotates in FP32).
+ */
+int qsrt_hadamard_f64(double *x, int64_t rows, int64_t cols, int64_t ld, int block, int side, const double *pre_mul,
+                      const double *pre_div, const double *post_mul, void *stream);
+
+/*
  * One matrix (or a run of record strips of a mixed-rate matrix) for
  * qsrt_decode.  The matrix is a grid of 128 x 128 blocks of 8 x 8 tiles;
  * tile (i, j) of block (R, C) starts at
@@ -252,6 +264,20 @@ int qsrt_gemm_tn_ws(float *C, const void *A, const void *B, const void *B2, int6
                     size_t workspace_bytes, void *stream);
 
 /*
+ *   C[M, N] += alpha * A^T (B - B2)      A: [K, M] f64, B: [K, N] f64,
+ *                                        B2: [K, N] f32 or NULL, C: [M, N] f64
+ * row-major with leading dimensions lda, ldb, ldb2, ldc (elements; even).
+ * A and B 16-byte aligned.  Float64 matrix cores (v_mfma_f64_16x16x4_f64);
+ * every element of C sums its K terms in the same order for any M and N.
+ * The BlockLDLQ product-cache update P += L[span]^T (W - Q)[span] under the
+ * encoder's float64 contract (factor and regularised weight float64, the
+ * reconstruction FP32).  Replaces the reference's FP32 span products
+ * (qsrt/exl3_encoder_backend.py:534, batched :1450-1471).
+ */
+int qsrt_gemm_tn_f64(double *C, const double *A, const double *B, const float *B2, int64_t M, int64_t N, int64_t K,
+                     int64_t lda, int64_t ldb, int64_t ldb2, int64_t ldc, double alpha, void *stream);
+
+/*
  * Diagonal-block step of a blocked float64 Cholesky factorisation, for
  * `batch` matrices A[b] = A + b * batch_stride (n x n, row-major, leading
  * dimension n).  The lower triangle of the nb x nb block at (j0, j0) is
@@ -310,10 +336,11 @@ int qsrt_bakron_band_update_lower_f32(float *workspace, const float *quantized, 
  * src[m]).  For the 16-row block [blk, blk + 16) of a span ending at row
  * `end`, every member's target
  *   T_m = W_s[blk] + mult[m] * (P_m[blk] + L_s[blk+16:end, blk:blk+16]^T (W_s - Q_m)[blk+16:end])
- * is written, one 16 x 16 tile per 16 columns in tensor-core order, to tile
- * slot[m * N/16 + t] of `tiles` ([slots, 256] f32; the caller groups slots
- * by rate).  W [S, K, N], L [S, K, K], Q and P [B, K, N]: row-major f32 with
- * batch strides sW, sL, sQ, sP (elements); src int32 [B] device, mult f32 [B]
+ * is computed in float64 and written, rounded once to FP32, one 16 x 16 tile
+ * per 16 columns in tensor-core order, to tile slot[m * N/16 + t] of `tiles`
+ * ([slots, 256] f32; the caller groups slots by rate).  W [S, K, N],
+ * L [S, K, K] and P [B, K, N] row-major f64, Q [B, K, N] row-major f32, with
+ * batch strides sW, sL, sQ, sP (elements); src int32 [B] device, mult f64 [B]
  * device, slot int32 [B * N/16] device.  K and N multiples of 16, blk a
  * multiple of 16 with blk + 16 <= end <= K.  Each element sums P first, then
  * the products in increasing row order, independent of B and N.
@@ -321,8 +348,8 @@ int qsrt_bakron_band_update_lower_f32(float *workspace, const float *quantized, 
  * stack and tensor-core gather of ldlq / ldlq_mixed_batched
  * (qsrt/exl3_encoder_backend.py:420-539, :1190-1478).
  */
-int qsrt_ldlq_targets(float *tiles, const float *W, const float *L, const float *Q, const float *P,
-                      const int32_t *src, const float *mult, const int32_t *slot, int B, int64_t K, int64_t N,
+int qsrt_ldlq_targets(float *tiles, const double *W, const double *L, const float *Q, const double *P,
+                      const int32_t *src, const double *mult, const int32_t *slot, int B, int64_t K, int64_t N,
                       int64_t sW, int64_t sL, int64_t sQ, int64_t sP, int64_t blk, int64_t end, void *stream);
 
 /*

@@ -104,15 +104,16 @@ def blockldlq(W_r: np.ndarray, L0: np.ndarray, tile_bits: np.ndarray, labels: di
 def encode_matrix(W: np.ndarray, H_sum: np.ndarray, count: int, su_signs: np.ndarray, sv_signs: np.ndarray,
                   g_scale: float, tile_bits: np.ndarray, labels: dict, lags: dict, *, sigma_reg: float,
                   conditioned: bool = False, g_into_sv: bool = False, input_scales: np.ndarray | None = None,
-                  context: int = 128, threads: int = 0) -> dict:
+                  apply_out_scales: bool = False, context: int = 128, threads: int = 0) -> dict:
     """The whole chain for one matrix.  ``conditioned`` selects the batch
     preparation (congruence with the regularised ``su`` before ``g``)
-    instead of the sign vector; ``g_into_sv`` and ``input_scales`` are the
-    w1/w3 options of ``regularize``.  Returns the ``blockldlq`` dict plus
-    ``W_r``, ``su``, ``sv``, ``H_c`` and ``L0``."""
+    instead of the sign vector; ``g_into_sv``, ``input_scales`` and
+    ``apply_out_scales`` are the options of ``regularize``.  Returns the
+    ``blockldlq`` dict plus ``W_r``, ``su``, ``sv``, ``H_c`` and ``L0``."""
 
     H = prepare_hessian(H_sum, count, sigma_reg)
-    W_r, su, sv = oldlq.regularize(W, su_signs, sv_signs, g_scale, g_into_sv=g_into_sv, input_scales=input_scales)
+    W_r, su, sv = oldlq.regularize(W, su_signs, sv_signs, g_scale, g_into_sv=g_into_sv, input_scales=input_scales,
+                                   apply_out_scales=apply_out_scales)
     if conditioned:
         s = su if g_into_sv else su * g_scale
     else:

@@ -10,16 +10,19 @@ Restates ``qsrt/exl3_encoder_backend.py``:
   L0 the strictly block-lower part -- pinned by the identity
   T - Q == (I + L0^T)(W - Q) for an arbitrary quantizer
   (``tests/test_blockldlq_proof.py:62-95``) and by a direct per-block loop;
-* ``regularize`` (:2580-2708) up to the global-scale search and the
-  Hessian congruence of ``_factor_capture_H`` (:2125-2160): no reference
-  test or fixture holds values for them (the reference backend cannot be
-  imported here).  They are pinned by the mathematics instead: the
-  congruence equals T H T^T with T = (I (x) H_128) D_su built densely from
-  scipy's Sylvester Hadamard, keeps H's spectrum and fixes I; the
-  regularisation is inverted exactly by the decoder's formula, gives every
-  128-row block an RMS of g * 1.24371088, and returns
-  su = -su rms_rows(W) / (1.24371088 g) in closed form.  The constant
-  1.24371088 itself is the reference's (:2580-2708).
+* ``regularize`` (:2580-2708) up to the global-scale search, its output-
+  scale rule ``out_scale_policy`` (:2605-2628) and the Hessian congruence
+  of ``_factor_capture_H`` (:2125-2160): no reference test or fixture holds
+  values for them (the reference backend cannot be imported here).  They
+  are pinned by the mathematics instead: the congruence equals T H T^T with
+  T = (I (x) H_128) D_su built densely from scipy's Sylvester Hadamard,
+  keeps H's spectrum and fixes I; the regularisation is inverted exactly by
+  the decoder's formula, gives every 128-row block an RMS of
+  g * 1.24371088, and returns su = -su rms_rows(W) / (1.24371088 g) in
+  closed form; with output scales every live column of W / sv has the mean
+  column RMS of W; the policy's share on a diagonal built from two values
+  has a closed form.  The constants 1.24371088, 2% and 15% are the
+  reference's (:2580-2708).
 """
 
 from __future__ import annotations
@@ -90,11 +93,29 @@ def congruence(H: np.ndarray, su_signs: np.ndarray) -> np.ndarray:
     return np.einsum("kbj,ji->kbi", M.reshape(k, k // 128, 128), h).reshape(k, k)
 
 
+def out_scale_policy(H_diag, forced, q_fallback: bool = False):
+    """Whether ``regularize`` applies output-channel scales (reference
+    :2605-2628): with a Hessian diagonal, when the largest 2% (``n // 50``)
+    of its square roots hold under 15% of their sum; ``forced`` (True or
+    False) overrides the rule; without a diagonal the default is True; a
+    fallback encode takes ``forced`` as it is."""
+
+    if q_fallback:
+        return forced
+    if H_diag is None:
+        return True if forced is None else forced
+    root = np.sort(np.sqrt(np.asarray(H_diag, dtype=np.float64).reshape(-1)))[::-1]
+    share = root[: root.shape[0] // 50].sum() / root.sum()
+    return bool(share < 0.15) if forced is None else forced
+
+
 def regularize(weight: np.ndarray, su_signs: np.ndarray, sv_signs: np.ndarray, g_scale: float, *,
-               g_into_sv: bool = False, input_scales: np.ndarray | None = None):
-    """Regularisation with apply_out_scales=False and a fixed global scale:
-    W /= sv; W <- W Had; su = su * rms_rows(W) / -1.24371088 + 1e-10;
-    W /= su; W <- Had W; W *= g; su /= g (sv /= g with ``g_into_sv``, as
+               g_into_sv: bool = False, input_scales: np.ndarray | None = None, apply_out_scales: bool = False):
+    """Regularisation at a fixed global scale: column RMS c of W normalised
+    to mean 1 (dead columns at 0.1), sv = sv * c + 1e-10 when
+    ``apply_out_scales``; W /= sv; sv of all-zero columns set to 0;
+    W <- W Had; su = su * rms_rows(W) / -1.24371088 + 1e-10; W /= su;
+    W <- Had W; W *= g; su /= g (sv /= g with ``g_into_sv``, as
     ``g_scale_into_sv`` does for w1/w3, :2727-2751).  ``input_scales``
     replaces rms_rows(W) by a layer-shared profile (the reference's
     ``shared_input_scales_key``, :2669-2672).  Returns (W, su, sv) in
@@ -105,7 +126,16 @@ def regularize(weight: np.ndarray, su_signs: np.ndarray, sv_signs: np.ndarray, g
     sv = np.asarray(sv_signs, dtype=np.float64).reshape(1, n).copy()
     su = np.asarray(su_signs, dtype=np.float64).reshape(k, 1)
     h = hadamard(128)
+    cols = np.sqrt((W * W).mean(axis=0, keepdims=True))
+    mean = float(cols.mean())
+    if mean > 1e-30:
+        cols = cols / mean
+    dead = np.abs(cols) < 1e-30
+    if apply_out_scales:
+        cols[dead] = 0.1
+        sv = sv * cols + 1e-10
     W /= sv
+    sv[dead] = 0.0
     W = np.einsum("kbj,ji->kbi", W.reshape(k, n // 128, 128), h).reshape(k, n)
     if input_scales is None:
         rms = np.sqrt((W * W).mean(axis=1, keepdims=True))

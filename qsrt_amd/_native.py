@@ -66,6 +66,11 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float,
          _c_int, _c_void_p, _c_size, _c_void_p],
     ),
+    "qsrt_gemm_tn_f64": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+         ctypes.c_double, _c_void_p],
+    ),
     "qsrt_chol_diag_block_f64": (
         _c_int, [_c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_void_p, _c_void_p, _c_void_p],
     ),
@@ -88,6 +93,10 @@ SIGNATURES: dict[str, tuple] = {
          _c_void_p],
     ),
     "qsrt_hadamard": (
+        _c_int,
+        [_c_void_p, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
+    ),
+    "qsrt_hadamard_f64": (
         _c_int,
         [_c_void_p, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
     ),

@@ -43,4 +43,4 @@ int current_cu_count(int* out) {
 
 extern "C" const char* qsrt_last_error(void) { return qsrt::g_last_error; }
 
-extern "C" int qsrt_abi_version(void) { return 1; }
+extern "C" int qsrt_abi_version(void) { return 2; }

@@ -598,3 +598,180 @@ int qsrt_gemm_tn(float* C, const void* A, const void* B, const void* B2, int64_t
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------- FP64 path
+// C[M, N] += alpha * A^T (B - B2) with A, B, C float64 and B2 FP32: the
+// BlockLDLQ product cache P += L[span]^T (W - Q)[span] under the encoder's
+// float64 contract (the factor L and the regularised weight W stay float64,
+// the reconstruction Q is FP32 labels, exact in float64), so that the
+// targets the tile Viterbi sees are the float64 sums rounded once.
+//
+// v_mfma_f64_16x16x4_f64: lane l holds A[m = l % 16][k = l / 16] and
+// B[k = l / 16][n = l % 16]; its accumulator r is C[l / 16 + 4 r][l % 16] (rows
+// interleaved by four, unlike the FP32 16x16x4 form's C[4 (l / 16) + r]).
+// One 256-thread workgroup per 128 x 128 tile of C (four waves of 64 x 64,
+// sixteen 16 x 16 accumulator tiles each, 128 accumulator registers), K in
+// chunks of 16 rows staged through double-buffered LDS, the next chunk's
+// global loads issued before the current chunk's products.  Each element of
+// C sums its K terms in increasing chunk order, the same for any M and N, so
+// a column's result does not depend on the width of the launch.
+namespace {
+
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBK64 = 16;
+constexpr int kPad64 = 16;  // row pad (doubles): the four k-rows of a fragment read start 32 banks apart
+
+struct F64Chunk {
+    double2 a[4], b[4];
+};
+
+__device__ __forceinline__ double2 ld2_masked(const double* p, int64_t row, int64_t col, int64_t rows, int64_t cols,
+                                              int64_t ld) {
+    if (row >= rows) return make_double2(0.0, 0.0);
+    const double* q = p + row * ld + col;
+    if (col + 1 < cols) return *reinterpret_cast<const double2*>(q);
+    return make_double2(col < cols ? q[0] : 0.0, 0.0);
+}
+
+__device__ __forceinline__ double2 ld2_masked_f32(const float* p, int64_t row, int64_t col, int64_t rows,
+                                                  int64_t cols, int64_t ld) {
+    if (row >= rows) return make_double2(0.0, 0.0);
+    const float* q = p + row * ld + col;
+    if (col + 1 < cols) {
+        const float2 v = *reinterpret_cast<const float2*>(q);
+        return make_double2(v.x, v.y);
+    }
+    return make_double2(col < cols ? static_cast<double>(q[0]) : 0.0, 0.0);
+}
+
+__device__ __forceinline__ void load_f64(F64Chunk& ch, const double* A, const double* B, const float* B2, int64_t k0,
+                                         int64_t m0, int64_t n0, int64_t M, int64_t N, int64_t K, int64_t lda,
+                                         int64_t ldb, int64_t ldb2, int t) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int f = t + kThreads * i;  // 1024 double2 per operand chunk: 16 rows x 64 double2
+        const int r = f >> 6, q = f & 63;
+        ch.a[i] = ld2_masked(A, k0 + r, m0 + 2 * q, K, M, lda);
+        double2 b = ld2_masked(B, k0 + r, n0 + 2 * q, K, N, ldb);
+        if (B2) {
+            const double2 s = ld2_masked_f32(B2, k0 + r, n0 + 2 * q, K, N, ldb2);
+            b.x -= s.x;
+            b.y -= s.y;
+        }
+        ch.b[i] = b;
+    }
+}
+
+__device__ __forceinline__ void store_f64(const F64Chunk& ch, double (*As)[kBM + kPad64], double (*Bs)[kBN + kPad64],
+                                          int t) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int f = t + kThreads * i;
+        const int r = f >> 6, q = f & 63;
+        *reinterpret_cast<double2*>(&As[r][2 * q]) = ch.a[i];
+        *reinterpret_cast<double2*>(&Bs[r][2 * q]) = ch.b[i];
+    }
+}
+
+// Two waves per SIMD: 128 accumulator registers plus the operand chunk fit in 256.
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void gemm_tn_f64_kernel(double* __restrict__ C, const double* __restrict__ A,
+                                                               const double* __restrict__ B,
+                                                               const float* __restrict__ B2, int64_t M, int64_t N,
+                                                               int64_t K, int64_t lda, int64_t ldb, int64_t ldb2,
+                                                               int64_t ldc, double alpha, int64_t tiles_n) {
+    __shared__ __attribute__((aligned(16))) double As[2][kBK64][kBM + kPad64];
+    __shared__ __attribute__((aligned(16))) double Bs[2][kBK64][kBN + kPad64];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int c = lane & 15, g = lane >> 4;
+    const int64_t m0 = (blockIdx.x / tiles_n) * kBM, n0 = (blockIdx.x % tiles_n) * kBN;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+
+    const bool seed = alpha == 1.0;  // accumulators start from C (plain store at the end)
+    f64x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f64x4{0.0, 0.0, 0.0, 0.0};
+    if (seed) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t row = m0 + wm + 16 * i + g + 4 * r;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int64_t col = n0 + wn + 16 * j + c;
+                    if (row < M && col < N) acc[i][j][r] = C[row * ldc + col];
+                }
+            }
+    }
+
+    F64Chunk ch;
+    load_f64(ch, A, B, B2, 0, m0, n0, M, N, K, lda, ldb, ldb2, t);
+    store_f64(ch, As[0], Bs[0], t);
+    __syncthreads();
+    const int64_t chunks = (K + kBK64 - 1) / kBK64;
+    for (int64_t kc = 0; kc < chunks; ++kc) {
+        const int cur = kc & 1;
+        if (kc + 1 < chunks) load_f64(ch, A, B, B2, (kc + 1) * kBK64, m0, n0, M, N, K, lda, ldb, ldb2, t);
+#pragma unroll
+        for (int kk = 0; kk < kBK64 / 4; ++kk) {
+            double a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a[i] = As[cur][4 * kk + g][wm + 16 * i + c];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = Bs[cur][4 * kk + g][wn + 16 * j + c];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        if (kc + 1 < chunks) store_f64(ch, As[cur ^ 1], Bs[cur ^ 1], t);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t row = m0 + wm + 16 * i + g + 4 * r;
+            if (row >= M) continue;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t col = n0 + wn + 16 * j + c;
+                if (col < N) {
+                    if (seed)
+                        C[row * ldc + col] = acc[i][j][r];
+                    else
+                        C[row * ldc + col] += alpha * acc[i][j][r];
+                }
+            }
+        }
+}
+
+}  // namespace
+
+extern "C" {
+
+int qsrt_gemm_tn_f64(double* C, const double* A, const double* B, const float* B2, int64_t M, int64_t N, int64_t K,
+                     int64_t lda, int64_t ldb, int64_t ldb2, int64_t ldc, double alpha, void* stream_handle) {
+    if (M < 0 || N < 0 || K < 0) return qsrt::fail(qsrt::kBadArgument, "gemm f64: negative extent");
+    if (M == 0 || N == 0 || K == 0) return qsrt::kOk;
+    if (!C || !A || !B) return qsrt::fail(qsrt::kBadArgument, "null pointer argument");
+    if (lda < M || ldb < N || ldc < N || (B2 && ldb2 < N))
+        return qsrt::fail(qsrt::kBadArgument, "gemm f64: leading dimension smaller than the row");
+    if (lda % 2 || ldb % 2 || (B2 && ldb2 % 2) || reinterpret_cast<uintptr_t>(A) % 16 ||
+        reinterpret_cast<uintptr_t>(B) % 16 || (B2 && reinterpret_cast<uintptr_t>(B2) % 8))
+        return qsrt::fail(qsrt::kBadArgument,
+                          "gemm f64: A and B must be 16-byte aligned, B2 8-byte aligned, leading dimensions even");
+    const int64_t tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
+    if (tiles_m * tiles_n > 0x7fffffff) return qsrt::fail(qsrt::kBadArgument, "gemm f64: too many tiles");
+    hipLaunchKernelGGL(gemm_tn_f64_kernel, dim3(static_cast<unsigned>(tiles_m * tiles_n)), dim3(kThreads), 0,
+                       static_cast<hipStream_t>(stream_handle), C, A, B, B2, M, N, K, lda, ldb, ldb2, ldc, alpha,
+                       tiles_n);
+    QSRT_HIP_TRY(hipGetLastError());
+    return qsrt::kOk;
+}
+
+}  // extern "C"

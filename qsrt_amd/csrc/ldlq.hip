@@ -13,9 +13,11 @@
 // launch writes the reconstruction back into Q_m's rows and the states into
 // the member's encoded tile row.
 //
-// Sum order: every target element accumulates P first, then the products in
-// increasing row order, whatever the batch or matrix width -- so candidates
-// encoded in different batch shapes stay bit-identical.
+// Precision: W, L and P are float64 and Q is FP32 (exact labels); every sum is
+// float64 and the target is rounded to FP32 once, on its way into the tile
+// buffer.  Sum order: every target element accumulates P first, then the
+// products in increasing row order, whatever the batch or matrix width -- so
+// candidates encoded in different batch shapes stay bit-identical.
 
 #include "common.h"
 #include "qsrt_amd.h"
@@ -34,36 +36,36 @@ __device__ __forceinline__ int tc_pos(int r, int c) {
 }
 
 __global__ __launch_bounds__(kThreads) void ldlq_targets_kernel(
-    float* __restrict__ tiles, const float* __restrict__ W, const float* __restrict__ L, const float* __restrict__ Q,
-    const float* __restrict__ P, const int32_t* __restrict__ src, const float* __restrict__ mult,
-    const int32_t* __restrict__ slot, int64_t K, int64_t N, int64_t sW, int64_t sL, int64_t sQ, int64_t sP, int64_t blk,
-    int64_t rows) {
-    __shared__ float ls[kChunk][16];  // L_s[blk_end + j, blk + r]
-    __shared__ float ds[kChunk][17];  // (W_s - Q_m)[blk_end + j, 16 t + c], padded against bank conflicts
+    float* __restrict__ tiles, const double* __restrict__ W, const double* __restrict__ L,
+    const float* __restrict__ Q, const double* __restrict__ P, const int32_t* __restrict__ src,
+    const double* __restrict__ mult, const int32_t* __restrict__ slot, int64_t K, int64_t N, int64_t sW, int64_t sL,
+    int64_t sQ, int64_t sP, int64_t blk, int64_t rows) {
+    __shared__ double ls[kChunk][16];  // L_s[blk_end + j, blk + r]
+    __shared__ double ds[kChunk][17];  // (W_s - Q_m)[blk_end + j, 16 t + c], padded against bank conflicts
     const int t = blockIdx.x, m = blockIdx.y, nt = gridDim.x;
     const int tid = threadIdx.x, r = tid >> 4, c = tid & 15;
     const int64_t s = src[m];
-    const float* Ws = W + s * sW;
-    const float* Ls = L + s * sL;
+    const double* Ws = W + s * sW;
+    const double* Ls = L + s * sL;
     const float* Qm = Q + m * sQ;
     const int64_t e = (blk + r) * N + 16 * t + c;
-    float acc = P[m * sP + e];
+    double acc = P[m * sP + e];
     for (int64_t j0 = 0; j0 < rows; j0 += kChunk) {
         const int n = static_cast<int>(rows - j0 < kChunk ? rows - j0 : kChunk);
         for (int i = tid; i < n * 16; i += kThreads) {
             const int j = i >> 4, cc = i & 15;
             const int64_t row = blk + 16 + j0 + j;
             ls[j][cc] = Ls[row * K + blk + cc];
-            ds[j][cc] = Ws[row * N + 16 * t + cc] - Qm[row * N + 16 * t + cc];
+            ds[j][cc] = Ws[row * N + 16 * t + cc] - static_cast<double>(Qm[row * N + 16 * t + cc]);
         }
         __syncthreads();
-        for (int j = 0; j < n; ++j) acc = __builtin_fmaf(ls[j][r], ds[j][c], acc);
+        for (int j = 0; j < n; ++j) acc = __builtin_fma(ls[j][r], ds[j][c], acc);
         __syncthreads();
     }
-    const float w = Ws[e];
-    const float k = mult[m];
-    const float target = k == 1.0f ? w + acc : (k == 0.0f ? w : w + k * acc);
-    tiles[static_cast<int64_t>(slot[m * nt + t]) * 256 + tc_pos(r, c)] = target;
+    const double w = Ws[e];
+    const double k = mult[m];
+    const double target = k == 1.0 ? w + acc : (k == 0.0 ? w : w + k * acc);
+    tiles[static_cast<int64_t>(slot[m * nt + t]) * 256 + tc_pos(r, c)] = static_cast<float>(target);
 }
 
 __global__ __launch_bounds__(kThreads) void ldlq_commit_kernel(
@@ -80,8 +82,8 @@ __global__ __launch_bounds__(kThreads) void ldlq_commit_kernel(
 
 extern "C" {
 
-int qsrt_ldlq_targets(float* tiles, const float* W, const float* L, const float* Q, const float* P,
-                      const int32_t* src, const float* mult, const int32_t* slot, int B, int64_t K, int64_t N,
+int qsrt_ldlq_targets(float* tiles, const double* W, const double* L, const float* Q, const double* P,
+                      const int32_t* src, const double* mult, const int32_t* slot, int B, int64_t K, int64_t N,
                       int64_t sW, int64_t sL, int64_t sQ, int64_t sP, int64_t blk, int64_t end, void* stream) {
     if (B < 0 || K <= 0 || N <= 0 || N % 16 || K % 16)
         return qsrt::fail(qsrt::kBadArgument, "ldlq targets: need B >= 0 and K, N positive multiples of 16");

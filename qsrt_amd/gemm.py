@@ -1,10 +1,11 @@
 """Dense products of the BlockLDLQ recursion and of Hessian capture.
 
-Device tensors run the HIP matrix-core kernel behind ``qsrt_gemm_tn``
-(``include/qsrt_amd.h``): FP32 operands with exact products and FP32
-accumulation for the feedback ``C += A^T (B - B2)`` (reference
-``exl3_encoder_backend.py:496``, ``:534``, batched ``:1170-1187``), bf16
-operands for ``H += X^T X``.  CPU tensors use torch in FP32.
+Device tensors run the HIP matrix-core kernels behind ``qsrt_gemm_tn`` and
+``qsrt_gemm_tn_f64`` (``include/qsrt_amd.h``): the BlockLDLQ feedback
+``C += A^T (B - B2)`` (reference ``exl3_encoder_backend.py:496``, ``:534``,
+batched ``:1170-1187``) with float64 factor, weight and product cache and an
+FP32 reconstruction ``B2`` on the float64 matrix cores, or all-FP32 operands
+on the FP32 ones; bf16 operands for ``H += X^T X``.  CPU tensors use torch.
 """
 
 from __future__ import annotations
@@ -59,6 +60,8 @@ def addmm_sub_tn_(C: torch.Tensor, A: torch.Tensor, B: torch.Tensor, B2: torch.T
     K, M = A.shape
     if B.shape[0] != K or C.shape != (M, B.shape[1]) or (B2 is not None and B2.shape != B.shape):
         raise ValueError("addmm_sub_tn_: incompatible shapes")
+    if C.is_cuda and C.dtype == torch.float64:
+        return _addmm_sub_tn_f64_(C, A, B, B2, alpha)
     if C.is_cuda:
         if C.dtype != torch.float32 or A.dtype != torch.float32 or B.dtype != torch.float32:
             raise ValueError("addmm_sub_tn_: float32 operands expected")
@@ -72,8 +75,30 @@ def addmm_sub_tn_(C: torch.Tensor, A: torch.Tensor, B: torch.Tensor, B2: torch.T
             raise ValueError("addmm_sub_tn_: C must be row-major")
         _launch(C, A, B, B2, alpha, 0)
         return C
-    rhs = B if B2 is None else B - B2
-    return C.addmm_(A.T, rhs, alpha=alpha)
+    rhs = B if B2 is None else B - B2.to(B.dtype)
+    return C.addmm_(A.T, rhs.to(C.dtype), alpha=alpha)
+
+
+def _addmm_sub_tn_f64_(C, A, B, B2, alpha):
+    """Float64 ``C``, ``A``, ``B`` and an FP32 (or absent) ``B2`` on the
+    float64 matrix cores."""
+
+    if A.dtype != torch.float64 or B.dtype != torch.float64 or (B2 is not None and B2.dtype != torch.float32):
+        raise ValueError("addmm_sub_tn_: a float64 C takes float64 A and B and a float32 B2")
+    if not _row_major(C) or C.stride(0) % 2:
+        raise ValueError("addmm_sub_tn_: C must be row-major with an even leading dimension")
+    A, B = _aligned(A, 2), _aligned(B, 2)
+    if B2 is not None and (not _row_major(B2) or B2.stride(0) % 2 or B2.data_ptr() % 8):
+        B2 = _copy_padded(B2, (B2.shape[1] + 1) // 2 * 2)
+    K, M = A.shape
+    N = B.shape[1]
+    _native.check(
+        _native.lib().qsrt_gemm_tn_f64(C.data_ptr(), A.data_ptr(), B.data_ptr(), None if B2 is None else B2.data_ptr(),
+                                       M, N, K, A.stride(0), B.stride(0), 0 if B2 is None else B2.stride(0),
+                                       C.stride(0), float(alpha), _native.stream_handle(C.device)),
+        "qsrt_gemm_tn_f64",
+    )
+    return C
 
 
 def addmm_tn_(C: torch.Tensor, A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:

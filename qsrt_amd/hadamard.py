@@ -1,7 +1,8 @@
 """Blockwise normalised Hadamard rotations (128-row/column blocks for the
 EXL basis, 512/128 for the coupled expert basis).
 
-Device tensors run the HIP butterfly kernel behind ``qsrt_hadamard``
+Device tensors run the HIP butterfly kernel behind ``qsrt_hadamard`` (FP32)
+or ``qsrt_hadamard_f64`` (float64, the encoder's regularisation)
 (``include/qsrt_amd.h``); the optional per-index vectors fuse the sign and
 scale multiplies that surround each rotation.  CPU tensors use the same
 matrix definition with torch (the reference's functions accept both).
@@ -24,8 +25,8 @@ def _vec(v, n: int, x: torch.Tensor):
     v = v.reshape(-1)
     if v.numel() != n:
         raise ValueError("scale vector does not align with the rotated axis")
-    if v.device != x.device or v.dtype != torch.float32 or not v.is_contiguous():
-        v = v.to(device=x.device, dtype=torch.float32).contiguous()
+    if v.device != x.device or v.dtype != x.dtype or not v.is_contiguous():
+        v = v.to(device=x.device, dtype=x.dtype).contiguous()
     return v
 
 
@@ -33,10 +34,10 @@ def rotate_(x: torch.Tensor, block: int = 128, *, side: str, pre_mul=None, pre_d
     """In place: ``x[blk] = post_mul * (H @ (x[blk] * pre_mul / pre_div))``
     per ``block`` rows (``side="left"``), or the same per ``block`` columns
     with ``x[:, blk] @ H`` (``side="right"``).  Vectors are indexed along
-    the rotated axis."""
+    the rotated axis and taken in ``x``'s dtype (float32 or float64)."""
 
-    if x.dtype != torch.float32 or x.ndim != 2:
-        raise ValueError("Hadamard rotation expects a float32 matrix")
+    if x.dtype not in (torch.float32, torch.float64) or x.ndim != 2:
+        raise ValueError("Hadamard rotation expects a float32 or float64 matrix")
     if side not in _SIDES:
         raise ValueError("side must be 'left' or 'right'")
     k, n = x.shape
@@ -53,15 +54,16 @@ def rotate_(x: torch.Tensor, block: int = 128, *, side: str, pre_mul=None, pre_d
         if x.stride(1) != 1 or x.stride(0) % 4 or n % 4 or x.data_ptr() % 16:
             raise ValueError("device Hadamard needs a row-major, 16-byte aligned matrix with columns % 4 == 0")
         lib = _native.lib()
+        entry = lib.qsrt_hadamard if x.dtype == torch.float32 else lib.qsrt_hadamard_f64
         _native.check(
-            lib.qsrt_hadamard(
+            entry(
                 x.data_ptr(), k, n, x.stride(0), block, _SIDES[side],
                 None if pre_mul is None else pre_mul.data_ptr(),
                 None if pre_div is None else pre_div.data_ptr(),
                 None if post_mul is None else post_mul.data_ptr(),
                 _native.stream_handle(x.device),
             ),
-            "qsrt_hadamard",
+            "qsrt_hadamard" if x.dtype == torch.float32 else "qsrt_hadamard_f64",
         )
         return x
     shape = (ext, 1) if side == "left" else (1, ext)

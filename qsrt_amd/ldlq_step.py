@@ -7,6 +7,11 @@ Viterbi is two launches for the whole batch (``include/qsrt_amd.h``):
 their slots of the rate-grouped tile buffer, and ``qsrt_ldlq_commit`` writes
 the reconstruction and states back.  The product-cache update after each
 span stays a matrix-core product per member (``qsrt_amd.gemm``).
+
+Precision: the regularised weight, the factor and the product cache are
+float64 and the reconstruction FP32 (its labels are exact); each target is
+its float64 sum rounded once to FP32, the contract of the float64 CPU
+recursion the payloads are compared with.
 """
 
 from __future__ import annotations
@@ -17,18 +22,19 @@ from . import _native
 
 
 class LdlqStep:
-    """Device views of one traversal: sources ``weights [S, K, N]`` and
-    ``Ls [S, K, K]``; per member ``weights_q``, ``prod_cache [B, K, N]`` and
-    ``encoded [B, K/16, N/16, 256]``; member ``m`` reads source ``src[m]``
-    and scales its feedback by ``multipliers[m]``."""
+    """Device views of one traversal: float64 sources ``weights [S, K, N]``
+    and ``Ls [S, K, K]``; per member float32 ``weights_q``, float64
+    ``prod_cache [B, K, N]`` and ``encoded [B, K/16, N/16, 256]``; member
+    ``m`` reads source ``src[m]`` and scales its feedback by
+    ``multipliers[m]``."""
 
     def __init__(self, weights, Ls, weights_q, prod_cache, encoded, src, multipliers):
         S, K, N = weights.shape
         B = weights_q.shape[0]
-        for name, t, shape, dtype in (("weights", weights, (S, K, N), torch.float32),
-                                      ("Ls", Ls, (S, K, K), torch.float32),
+        for name, t, shape, dtype in (("weights", weights, (S, K, N), torch.float64),
+                                      ("Ls", Ls, (S, K, K), torch.float64),
                                       ("weights_q", weights_q, (B, K, N), torch.float32),
-                                      ("prod_cache", prod_cache, (B, K, N), torch.float32),
+                                      ("prod_cache", prod_cache, (B, K, N), torch.float64),
                                       ("encoded", encoded, (B, K // 16, N // 16, 256), torch.int16)):
             if tuple(t.shape) != shape or t.dtype != dtype or not t.is_contiguous() or not t.is_cuda:
                 raise ValueError(f"LDLQ step: {name} must be a contiguous {dtype} CUDA tensor of shape {shape}")
@@ -43,7 +49,7 @@ class LdlqStep:
         self.W, self.L, self.Q, self.P, self.E = weights, Ls, weights_q, prod_cache, encoded
         self.B, self.K, self.N = B, K, N
         self.src = torch.tensor(src, dtype=torch.int32, device=dev)
-        self.mult = torch.tensor([float(m) for m in multipliers], dtype=torch.float32, device=dev)
+        self.mult = torch.tensor([float(m) for m in multipliers], dtype=torch.float64, device=dev)
         self._stream = lambda: _native.stream_handle(dev)
 
     @property

@@ -36,5 +36,5 @@ def test_python_signatures_cover_the_header():
 
 def test_abi_version_and_error_string_without_gpu():
     lib = _native.lib()
-    assert lib.qsrt_abi_version() == 1
+    assert lib.qsrt_abi_version() == 2
     assert isinstance(lib.qsrt_last_error(), bytes)

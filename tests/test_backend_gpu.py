@@ -99,8 +99,11 @@ def test_ldlq_teacher_forced_parity(bits, monkeypatch):
         rows = tiles[:, perm_i].reshape(n // 16, 16, 16).transpose(1, 0, 2).reshape(16, n)
         targets[blk:blk + 16] = rows
     want = oldlq.feedback_targets(W.cpu().double().numpy(), L.cpu().double().numpy(), weight_q.cpu().double().numpy())
-    scale = np.abs(want).max()
-    assert np.max(np.abs(targets - want)) <= 1e-5 * scale
+    # each target is the float64 recursion's value rounded once to FP32 (rare one-ulp summation-order flips)
+    g = np.ascontiguousarray(targets, dtype=np.float32)
+    c = want.astype(np.float32)
+    ulps = np.abs(g.view(np.int32).astype(np.int64) - c.view(np.int32).astype(np.int64))
+    assert int(ulps.max()) <= 1 and int(np.count_nonzero(ulps)) <= 4
     # encoded states are the closed paths the kernel returned, and decode to Q
     enc = encoded.cpu()
     assert torch.equal(enc, reconstruct_trellis_states(enc.to(torch.int64) & ((1 << bits) - 1), bits))
@@ -193,7 +196,7 @@ def test_factored_hessian_stays_on_the_device():
     d = torch.arange(k)
     L_again[d, d] = 0
     assert torch.equal(H_again, shared["H"])
-    assert torch.allclose(L_again, shared["L"], rtol=0, atol=1e-6)
+    assert torch.allclose(L_again, shared["L"].float(), rtol=0, atol=1e-6)
     L_obj = shared["L"]
     _, proxy2, _ = be.quantize_qsrt(W.clone(), shared, _qa(3), False)
     assert shared["L"] is L_obj and proxy2 == pytest.approx(proxy, rel=1e-6)

@@ -72,7 +72,8 @@ def test_finalize_capture_H_on_device_matches_float64_congruence_and_block_ldl()
     errs = (_rel(diag.cpu(), np.diag(Hp)), _rel(H.cpu(), H_c), _rel(L.cpu(), L0))
     _say(f"[backend-oracle] diag {errs[0]:.2e}, conditioned H {errs[1]:.2e}, L {errs[2]:.2e} (max rel)")
     assert np.array_equal(su.cpu().numpy().reshape(-1), s)
-    assert errs[0] <= 1e-6 and errs[1] <= 1e-5 and errs[2] <= 1e-5
+    assert L.dtype == torch.float64  # the factor stays float64; the metric is the FP32 rounding of H_c
+    assert errs[0] <= 1e-6 and errs[1] <= 1e-6 and errs[2] <= 1e-11
 
     # the conditioned (two-stage) preparation with a scaled su
     shared2 = make_shared_h(k, DEV, H_sum)
@@ -83,7 +84,7 @@ def test_finalize_capture_H_on_device_matches_float64_congruence_and_block_ldl()
     H_c2, L02 = oenc.factor(Hp, su_full.double().numpy())
     e2 = (_rel(H2.cpu(), H_c2), _rel(L2.cpu(), L02))
     _say(f"[backend-oracle] conditioned with scaled su: H {e2[0]:.2e}, L {e2[1]:.2e}")
-    assert e2[0] <= 1e-5 and e2[1] <= 1e-5
+    assert e2[0] <= 1e-6 and e2[1] <= 1e-11
 
 
 def _regularize_gpu(W, su, sv, qa):
@@ -102,10 +103,11 @@ def test_regularize_on_device_matches_oracle_at_fixed_scale():
     qa = {"apply_out_scales": False, "g_scale_override": 0.87}
     apply_out, W_r, g, su_r, sv_r = _regularize_gpu(W, su, sv, qa)
     assert apply_out is False and g == pytest.approx(0.87) and qa["zeros"] is False
+    assert W_r.dtype == su_r.dtype == sv_r.dtype == torch.float64
     W_o, su_o, sv_o = oldlq.regularize(W.double().numpy(), su, sv, 0.87)
     errs = (_rel(W_r.cpu(), W_o), _rel(su_r.cpu(), su_o), _rel(sv_r.cpu(), sv_o))
     _say(f"[backend-oracle] W_r {errs[0]:.2e}, su {errs[1]:.2e}, sv {errs[2]:.2e} (max rel)")
-    assert errs[0] <= 2e-6 and errs[1] <= 1e-6 and errs[2] == 0.0
+    assert errs[0] <= 1e-13 and errs[1] <= 1e-14 and errs[2] == 0.0
 
     # w1/w3: a layer-shared input profile (taken from the first matrix) and g folded into sv
     key = ("backend-oracle-test", "w1")
@@ -120,50 +122,33 @@ def test_regularize_on_device_matches_oracle_at_fixed_scale():
                                            input_scales=shared_profile)
         errs = (_rel(W_r.cpu(), W_o), _rel(su_r.cpu(), su_o), _rel(sv_r.cpu(), sv_o))
         _say(f"[backend-oracle] shared profile: W_r {errs[0]:.2e}, su {errs[1]:.2e}, sv {errs[2]:.2e}")
-        assert errs[0] <= 2e-6 and errs[1] <= 1e-6 and errs[2] <= 1e-7
+        assert errs[0] <= 1e-13 and errs[1] <= 1e-14 and errs[2] <= 1e-15
     be._SHARED_INPUT_SCALES.pop(key, None)
 
 
 @pytest.mark.parametrize("apply_out", [False, True])
-def test_regularize_fused_division_equals_two_step(apply_out):
-    """The device regularize divides by sv and su inside the rotation kernel
-    (its pre-divisor).  That must be the separate correctly rounded divide
-    followed by the rotation, bit for bit, dead channels included."""
-
-    from qsrt_amd import hadamard
+def test_regularize_on_device_matches_oracle_with_output_scales_and_dead_channels(apply_out):
+    """The device regularize (its divisions fused into the float64 rotation
+    kernel) against ``oracle.ldlq.regularize``, whose output-scale branch
+    is pinned by closed forms in ``test_ldlq_oracle.py``: with and without
+    output scales, with an all-zero output channel (its sv zeroed) and an
+    all-zero input row (its scale at 0.1)."""
 
     k, n = 512, 768
+    _say(f"[backend-oracle] regularize [{k} x {n}], apply_out_scales={apply_out}, dead channels")
     gen = torch.Generator().manual_seed(72)
-    W = bench.student_t_like((k, n), std=0.02, gen=gen)
+    W = bench.student_t_like((k, n), std=0.02, gen=gen) * torch.linspace(0.3, 3.0, n)[None, :]
     W[:, 5] = 0.0  # a dead output channel
-    W[7, :] = 0.0
-    su = torch.from_numpy(_signs(k, 8)).float().reshape(-1, 1).to(DEV)
-    sv = torch.from_numpy(_signs(n, 9)).float().reshape(1, -1).to(DEV)
+    W[7, :] = 0.0  # a dead input channel
+    su, sv = _signs(k, 8), _signs(n, 9)
     qa = {"apply_out_scales": apply_out, "g_scale_override": 0.9}
-    _, W_r, g, su_r, sv_r = be.regularize(W.to(DEV).clone(), su.clone(), sv.clone(), qa, False, None, None)
-    # the same steps as separate kernels
-    w = W.to(DEV).clone()
-    scales = be.block_rms(w, dim=0, keepdim=True)
-    scales /= scales.mean().item()  # a host scalar, as regularize divides (torch multiplies by its reciprocal)
-    dead = scales.abs() < 1e-30
-    sv2 = sv.clone()
-    if apply_out:
-        scales[dead] = 0.1
-        sv2 = (sv2 * scales + 1e-10).float()
-    w /= sv2
-    sv2[dead] = 0.0
-    hadamard.rotate_(w, 128, side="right")
-    rows = be.block_rms(w, dim=1, keepdim=True)
-    rows[rows.abs() < 1e-30] = 0.1
-    su2 = (su * rows / (-be.codebook_scale) + 1e-10).float()
-    w /= su2
-    hadamard.rotate_(w, 128, side="left")
-    w *= g
-    su2 /= g
-    torch.cuda.synchronize()
-    assert torch.equal(W_r, w)
-    assert torch.equal(su_r, su2)
-    assert torch.equal(sv_r, sv2)
+    applied, W_r, g, su_r, sv_r = _regularize_gpu(W, su, sv, qa)
+    assert applied is apply_out and g == pytest.approx(0.9)
+    W_o, su_o, sv_o = oldlq.regularize(W.double().numpy(), su, sv, 0.9, apply_out_scales=apply_out)
+    errs = (_rel(W_r.cpu(), W_o), _rel(su_r.cpu(), su_o), _rel(sv_r.cpu(), sv_o))
+    _say(f"[backend-oracle] W_r {errs[0]:.2e}, su {errs[1]:.2e}, sv {errs[2]:.2e} (max rel)")
+    assert errs[0] <= 1e-13 and errs[1] <= 1e-14 and errs[2] <= 1e-15
+    assert float(sv_r[0, 5]) == 0.0
 
 
 def _problem(k: int, n: int, seed: int):
@@ -193,6 +178,20 @@ def _record(monkeypatch):
 
     monkeypatch.setattr(be, "quantize_tiles_multigpu", recording)
     return calls
+
+
+def _assert_rounded_once(targets: np.ndarray, want: np.ndarray) -> None:
+    """GPU targets (the Viterbi's FP32 inputs) against the float64
+    recursion: each the float64 value rounded once to FP32, except rare
+    elements one ulp away (a float64 sum in another order on the other side
+    of a rounding boundary)."""
+
+    g = np.ascontiguousarray(targets, dtype=np.float32)
+    c = np.ascontiguousarray(want).astype(np.float32)
+    ulps = np.abs(g.view(np.int32).astype(np.int64) - c.view(np.int32).astype(np.int64))
+    _say(f"[backend-oracle] targets: {int(np.count_nonzero(ulps))} of {g.size} one ulp from the float64 "
+         f"recursion rounded once (max {int(ulps.max())})")
+    assert int(ulps.max()) <= 1 and int(np.count_nonzero(ulps)) <= max(4, g.size // 100_000)
 
 
 def _replay_and_targets(calls, members, tile_bits_of):
@@ -233,9 +232,8 @@ def test_ldlq_mixed_teacher_forced_per_rate(monkeypatch):
     torch.cuda.synchronize()
     targets = _replay_and_targets(calls, [(k // 16, n // 16)], lambda m, rb, t: nmap[t])[0]
     want = oldlq.feedback_targets(W.cpu().double().numpy(), L.cpu().double().numpy(), Q.cpu().double().numpy())
-    err = _rel(targets, want)
-    _say(f"[backend-oracle] {len(calls)} tile calls replayed bit-exactly; targets max rel {err:.2e}")
-    assert err <= 1e-5
+    _say(f"[backend-oracle] {len(calls)} tile calls replayed bit-exactly")
+    _assert_rounded_once(targets, want)
 
     calls.clear()
     kmap = [4, 3, 2, 3] * 4
@@ -243,7 +241,7 @@ def test_ldlq_mixed_teacher_forced_per_rate(monkeypatch):
     torch.cuda.synchronize()
     targets = _replay_and_targets(calls, [(k // 16, n // 16)], lambda m, rb, t: kmap[rb])[0]
     want = oldlq.feedback_targets(W.cpu().double().numpy(), L.cpu().double().numpy(), Q.cpu().double().numpy())
-    assert _rel(targets, want) <= 1e-5
+    _assert_rounded_once(targets, want)
 
 
 def test_ldlq_mixed_batched_teacher_forced_per_rate(monkeypatch):
@@ -258,9 +256,8 @@ def test_ldlq_mixed_batched_teacher_forced_per_rate(monkeypatch):
     targets = _replay_and_targets(calls, [(k // 16, n // 16)] * 2, lambda m, rb, t: maps[m][t])
     for m, (W, L) in enumerate(((W0, L0), (W1, L1))):
         want = oldlq.feedback_targets(W.cpu().double().numpy(), L.cpu().double().numpy(), Q[m].cpu().double().numpy())
-        err = _rel(targets[m], want)
-        _say(f"[backend-oracle] member {m}: targets max rel {err:.2e}")
-        assert err <= 1e-5
+        _say(f"[backend-oracle] member {m}")
+        _assert_rounded_once(targets[m], want)
 
 
 def test_l4_stored_payload_decodes_through_the_oracle_container_reader():

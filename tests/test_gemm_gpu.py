@@ -191,3 +191,51 @@ def test_gemm_rejects_bad_arguments():
     A = torch.randn(4, 4).cuda()
     with pytest.raises(ValueError):
         gemm.addmm_sub_tn_(torch.zeros(4, 5).cuda(), A, torch.randn(4, 4).cuda())
+
+
+@pytest.mark.parametrize("M,N,K", [(16, 256, 112), (200, 300, 77), (128, 128, 16), (2, 6, 3), (640, 2048, 128),
+                                   (96, 200, 129), (7040, 256, 128)])
+def test_float64_feedback_product_matches_float64(M, N, K):
+    """qsrt_gemm_tn_f64: C (f64) += alpha A^T (B - B2) with float64 A, B and
+    an FP32 B2 on the float64 matrix cores, against the same product on the
+    CPU; both sides are float64, so they agree to float64 rounding."""
+
+    print(f"[gemm] f64 M{M} N{N} K{K}", file=sys.stderr, flush=True)
+    g = torch.Generator().manual_seed(M * 5 + N + K)
+    A = torch.randn(K, M, generator=g, dtype=torch.float64)
+    B = torch.randn(K, N, generator=g, dtype=torch.float64)
+    B2 = torch.randn(K, N, generator=g)
+    C = torch.randn(M, N, generator=g, dtype=torch.float64)
+    for alpha, b2 in ((1.0, B2), (0.5, B2), (1.0, None)):
+        rhs = B.numpy() - (0.0 if b2 is None else b2.double().numpy())
+        want = C.numpy() + alpha * (A.numpy().T @ rhs)
+        Cg = C.cuda()
+        gemm.addmm_sub_tn_(Cg, A.cuda(), B.cuda(), None if b2 is None else b2.cuda(), alpha=alpha)
+        assert _rel(Cg.cpu().numpy(), want) < 1e-13
+
+
+def test_float64_span_update_is_width_independent():
+    """Each column of C sums its K terms in one order whatever N is: a column
+    block computed in a narrow launch equals the same columns of a wide one
+    bit for bit (the candidate-reuse paths of the recursion rely on it), and
+    repeated calls are identical."""
+
+    g = torch.Generator().manual_seed(5)
+    k, n, begin, end = 1024, 2048, 768, 896
+    L = torch.randn(k, k, generator=g, dtype=torch.float64).cuda()
+    W = torch.randn(k, n, generator=g, dtype=torch.float64).cuda()
+    Q = torch.randn(k, n, generator=g).cuda()
+    P0 = torch.randn(k, n, generator=g, dtype=torch.float64).cuda()
+    wide = P0.clone()
+    gemm.addmm_sub_tn_(wide[:begin], L[begin:end, :begin], W[begin:end], Q[begin:end])
+    again = P0.clone()
+    gemm.addmm_sub_tn_(again[:begin], L[begin:end, :begin], W[begin:end], Q[begin:end])
+    assert torch.equal(wide, again)
+    cols = slice(336, 336 + 48)
+    narrow = P0[:, cols].contiguous()
+    gemm.addmm_sub_tn_(narrow[:begin], L[begin:end, :begin], W[begin:end, cols].contiguous(),
+                       Q[begin:end, cols].contiguous())
+    assert torch.equal(narrow, wide[:, cols])
+    want = P0[:begin].cpu().numpy() + L[begin:end, :begin].cpu().numpy().T @ (
+        W[begin:end].cpu().numpy() - Q[begin:end].double().cpu().numpy())
+    assert _rel(wide[:begin].cpu().numpy(), want) < 1e-13

@@ -104,3 +104,23 @@ def test_coupled_basis_on_device_matches_cpu_path():
     h13 = rows.T @ rows
     tr = ex.transform_inputs(rows.cuda())
     assert torch.allclose(ex.transform_h13(h13.cuda()).cpu(), (tr.T @ tr).cpu(), rtol=1e-4, atol=1e-3)
+
+
+@pytest.mark.parametrize("block,side", [(b, s) for b in (64, 128, 256, 512) for s in ("left", "right")])
+def test_float64_hadamard_matches_float64(block, side):
+    """qsrt_hadamard_f64 (the regularisation's rotation) against the float64
+    Sylvester product, with fused pre-division and post-scale: float64 on
+    both sides, so they agree to float64 rounding."""
+
+    print(f"[hadamard] f64 block {block} {side}", file=sys.stderr, flush=True)
+    rows, cols = (1024, 516) if side == "left" else (516, 1024)
+    g = torch.Generator().manual_seed(block * 11 + rows)
+    x = torch.randn(rows, cols, generator=g, dtype=torch.float64)
+    ext = rows if side == "left" else cols
+    div = torch.rand(ext, generator=g, dtype=torch.float64) + 0.5
+    post = torch.randn(ext, generator=g, dtype=torch.float64)
+    got = x.cuda()
+    hadamard.rotate_(got, block, side=side, pre_div=div.cuda(), post_mul=post.cuda())
+    want = _want(x.numpy(), block, side, pre_div=div.numpy(), post_mul=post.numpy())
+    assert got.dtype == torch.float64
+    assert np.max(np.abs(got.cpu().numpy() - want)) <= 1e-14 * np.abs(want).max()

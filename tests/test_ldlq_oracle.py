@@ -95,8 +95,13 @@ def test_backend_regularize_matches_oracle_with_fixed_scale():
     _, w_r, g, su_r, sv_r = be.regularize(w, su.clone(), sv.clone(), qa, False, None, None)
     W_ref, su_ref, sv_ref = oldlq.regularize(W, su.numpy(), sv.numpy(), 0.8)
     assert g == 0.8
-    assert np.allclose(w_r.double().numpy(), W_ref, rtol=1e-5, atol=1e-6 * np.abs(W_ref).max())
-    assert np.allclose(su_r.double().numpy(), su_ref, rtol=1e-5)
+    assert w_r.dtype == torch.float64 and su_r.dtype == torch.float64
+    # float64 on both sides: the two differ only in the order of the rotations' sums
+    assert np.allclose(w_r.numpy(), W_ref, rtol=1e-12, atol=1e-13 * np.abs(W_ref).max())
+    assert np.allclose(su_r.numpy(), su_ref, rtol=1e-12)
+    assert np.array_equal(sv_r.numpy(), sv_ref)
+    # the caller's FP32 weight ends as the FP32 rounding of the regularised weight
+    assert torch.equal(w, w_r.float())
     assert qa["zeros"] is False
 
 
@@ -160,3 +165,82 @@ def test_oracle_regularize_pinned_by_inverse_and_closed_forms():
         if nonzero[rows].all():
             assert np.isclose(np.sqrt(np.mean(Wr[rows] ** 2)), g * c, rtol=1e-8)
     assert np.array_equal(sv_out.reshape(-1), sv)
+
+
+def test_oracle_out_scale_policy_closed_form_share():
+    # n // 50 = 10 entries of a, 490 of b: the top-2% share of the root diagonal is
+    # 10 sqrt(a) / (10 sqrt(a) + 490 sqrt(b)); scaling the diagonal leaves it unchanged, the order of the
+    # entries must not matter (a planted ascending sort reads the smallest 2% and flips both cases), and a
+    # forced value or a fallback encode overrides the rule
+    n, b = 500, 1.0
+    for share, expect in ((0.149, True), (0.151, False)):
+        ratio = share * 490.0 / (10.0 * (1.0 - share))  # sqrt(a) / sqrt(b)
+        diag = np.full(n, b)
+        diag[:10] = ratio ** 2 * b
+        rng = np.random.default_rng(3)
+        for d in (diag, rng.permutation(diag), 7.5 * diag):
+            assert oldlq.out_scale_policy(d, None) is expect
+            assert oldlq.out_scale_policy(d, not expect) is (not expect)
+    assert oldlq.out_scale_policy(None, None) is True
+    assert oldlq.out_scale_policy(None, False) is False
+    assert oldlq.out_scale_policy(np.ones(n), None, q_fallback=True) is None
+
+
+def test_oracle_regularize_output_scales_pinned_by_equal_column_rms():
+    # with output scales, sv = sign * colRMS / mean(colRMS) + 1e-10, so every live column of W / sv has the
+    # same RMS, mean(colRMS) -- not 1 (a missing mean normalisation fails) and not row-derived (a row RMS
+    # fails); an all-zero column gets sv = 0 and stays zero; the decoder's inverse returns W
+    k, n, g = 256, 384, 0.7
+    rng = np.random.default_rng(17)
+    W = rng.standard_t(5, size=(k, n)) * 0.02 * np.linspace(0.3, 3.0, n)[None, :]
+    W[:, 11] = 0.0
+    su = np.sign(rng.standard_normal(k))
+    sv = np.sign(rng.standard_normal(n))
+    Wr, su_out, sv_out = oldlq.regularize(W, su, sv, g, apply_out_scales=True)
+    cols = np.sqrt((W * W).mean(axis=0))
+    live = cols > 0
+    assert sv_out.reshape(-1)[11] == 0.0
+    assert np.array_equal(np.sign(sv_out.reshape(-1)[live]), sv[live])
+    scaled = W[:, live] / sv_out.reshape(-1)[live]
+    assert np.allclose(np.sqrt((scaled * scaled).mean(axis=0)), cols.mean(), rtol=1e-8)
+    assert not np.isclose(cols.mean(), 1.0)
+    TL = _block_had_signs(k, np.ones(k))
+    TR = _block_had_signs(n, np.ones(n))
+    back = ((su_out.reshape(k, 1) * (TL.T @ Wr)) @ TR.T) * sv_out.reshape(1, n)
+    assert np.allclose(back, W, atol=1e-12)
+    # without output scales the signs pass through, but the dead column's sv is still zeroed
+    _, _, sv_plain = oldlq.regularize(W, su, sv, g)
+    expect = sv.copy()
+    expect[11] = 0.0
+    assert np.array_equal(sv_plain.reshape(-1), expect)
+
+
+def test_backend_out_scale_policy_matches_oracle():
+    n = 500
+    for share in (0.149, 0.151):
+        ratio = share * 490.0 / (10.0 * (1.0 - share))
+        diag = np.ones(n)
+        diag[:10] = ratio ** 2
+        d = torch.from_numpy(diag).float()
+        for forced in (None, True, False):
+            assert be._out_scale_policy(d, forced, False, False) == oldlq.out_scale_policy(diag, forced)
+    assert be._out_scale_policy(None, None, False, False) is True
+    assert be._out_scale_policy(torch.ones(n), None, True, False) is None
+
+
+def test_backend_regularize_output_scales_matches_oracle_on_cpu():
+    rng = np.random.default_rng(19)
+    W = (rng.standard_t(5, size=(256, 384)) * 0.02).astype(np.float32)
+    W[:, 5] = 0.0
+    W[9, :] = 0.0
+    su = torch.from_numpy(np.sign(rng.standard_normal((256, 1))).astype(np.float32))
+    sv = torch.from_numpy(np.sign(rng.standard_normal((1, 384))).astype(np.float32))
+    for apply in (True, False):
+        qa = {"apply_out_scales": apply, "g_scale_override": 0.6}
+        applied, w_r, _, su_r, sv_r = be.regularize(torch.from_numpy(W.copy()), su.clone(), sv.clone(), qa, False,
+                                                    None, None)
+        W_ref, su_ref, sv_ref = oldlq.regularize(W, su.numpy(), sv.numpy(), 0.6, apply_out_scales=apply)
+        assert applied is apply
+        assert np.allclose(w_r.numpy(), W_ref, rtol=1e-12, atol=1e-13 * np.abs(W_ref).max())
+        assert np.allclose(su_r.numpy(), su_ref, rtol=1e-12)
+        assert np.allclose(sv_r.numpy(), sv_ref, rtol=1e-14, atol=0)
