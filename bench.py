@@ -178,11 +178,16 @@ def zipf_token_counts(experts: int = LAYER_EXPERTS, tokens: int = LAYER_TOKENS, 
 
 def expert_source(cfg: int, device, *, expert: int = 0, tokens: int | None = None) -> dict:
     """One expert's encoder inputs as they sit in HBM: bf16 weights and bf16
-    calibration rows (the activations a capture hook sees)."""
+    calibration rows (the activations a capture hook sees), plus each routed
+    row's gate value (uniform in [0.05, 1), from a generator of its own so
+    the weights and rows are unchanged; BASELINE does not fix them)."""
 
     d = config_expert(cfg, device, expert=expert, tokens=tokens)
+    n = int(d["x"].shape[0])
+    gen = torch.Generator(device=device).manual_seed((20261201 + cfg) * 1000 + expert + 500_000)
+    gates = 0.05 + 0.95 * torch.rand(n, generator=gen, device=device)
     return {"expert": expert, "w": tuple(d[k].bfloat16() for k in ("w_gate", "w_up", "w_down")),
-            "x": d["x"].bfloat16(), "tokens": int(d["x"].shape[0])}
+            "x": d["x"].bfloat16(), "tokens": n, "gates": gates}
 
 
 # ---------------------------------------------------------------------------
@@ -209,13 +214,29 @@ class ExpertEncoder:
     the H13 capture, one ``quantize_qsrt_batch`` over every gate and up
     matrix of the batch, H2 from the reconstructed gate/up SwiGLU
     activations, one ``quantize_qsrt_batch`` over the down matrices, and
-    record-major packing of every payload."""
+    record-major packing of every payload.
 
-    def __init__(self, device, *, hidden: int, inter: int, record_bits, layer: int = LAYER_ID, scope=None):
+    ``hessian_policy``: ``"routed"`` (default) takes H13
+    as the Gram of the expert's routed rows and H2 as the Gram of its decoded
+    post-activation rows.  ``"support_aware"`` is the production covariance
+    policy of ``qsrt_amd.candidate_hessian.build_expert_hessians``: H13 is
+    the layer's ``global_h13`` (the covariance of all the layer's
+    calibration rows), H2 the gate-square weighted covariance of the decoded
+    post-activation rows, OAS-shrunk toward its trace-scaled identity -- for
+    a low-support expert (tens of routed rows) mostly the identity.  The
+    evidence of each expert's H2 is kept in ``self.h2_evidence``."""
+
+    def __init__(self, device, *, hidden: int, inter: int, record_bits, layer: int = LAYER_ID, scope=None,
+                 hessian_policy: str = "routed", global_h13: torch.Tensor | None = None):
         from qsrt_amd.qsrt_coupled import CoupledHadamardSpec
 
         if inter % 128 or len(record_bits) != inter // 128:
             raise ValueError("one record rate per 128 intermediate channels")
+        if hessian_policy not in ("routed", "support_aware"):
+            raise ValueError("hessian_policy must be 'routed' or 'support_aware'")
+        if hessian_policy == "support_aware" and (global_h13 is None or tuple(global_h13.shape) != (hidden, hidden)):
+            raise ValueError("the support-aware policy needs the layer's global H13 [hidden, hidden]")
+        self.policy, self.global_h13, self.h2_evidence = hessian_policy, global_h13, {}
         self.dev, self.hidden, self.inter, self.layer = device, hidden, inter, layer
         self.record_bits = tuple(record_bits)
         self.rate_map = tuple(b for b in self.record_bits for _ in range(8))  # per 16-channel tile
@@ -247,18 +268,24 @@ class ExpertEncoder:
         from qsrt_amd.qsrt_coupled import coupled_execution, decode_coupled_weights, encode_coupled_weights
 
         dev, hidden, inter = self.dev, self.hidden, self.inter
+        aware = self.policy == "support_aware"
         prepared = []
         for src in sources:
             w = tuple(t.float() for t in src["w"])
             g_c, u_c, d_c = encode_coupled_weights(w, self.spec)
             ex = coupled_execution((g_c, u_c, d_c), self.spec)
-            h13 = ex.transform_h13(gemm.gram_(torch.zeros((hidden, hidden), device=dev), src["x"]))
-            prepared.append({"c": (g_c, u_c, d_c), "ex": ex, "h13": h13, "x": src["x"], "n": src["tokens"]})
+            if aware:  # the layer's global input covariance (local weight 0), already normalised
+                h13, count13 = ex.transform_h13(self.global_h13.to(dev).float()), 1
+            else:
+                h13 = ex.transform_h13(gemm.gram_(torch.zeros((hidden, hidden), device=dev), src["x"]))
+                count13 = src["tokens"]
+            prepared.append({"c": (g_c, u_c, d_c), "ex": ex, "h13": h13, "x": src["x"], "n": src["tokens"],
+                             "n13": count13, "gates": src.get("gates"), "expert": src["expert"]})
         weights, hs, qas = [], [], []
         for p in prepared:
             for name, m in (("w1", p["c"][0]), ("w3", p["c"][1])):
                 shared = make_shared_h(hidden, dev, p["h13"])
-                shared["count"] = p["n"]
+                shared["count"] = p["n13"]
                 weights.append(m.T.contiguous())
                 hs.append(shared)
                 qas.append([self.quant_args(name)])
@@ -276,10 +303,20 @@ class ExpertEncoder:
             gs, us, _ = decode_coupled_weights((g_hat, u_hat, p["c"][2]), self.spec)
             x = p["x"].float()
             h = (torch.nn.functional.silu(x @ gs.T) * (x @ us.T)).contiguous()
-            h2 = p["ex"].transform_h2(gemm.gram_(torch.zeros((inter, inter), device=dev), h))
+            if aware:
+                from qsrt_amd.candidate_hessian import build_expert_hessians
+
+                if p["gates"] is None:
+                    raise ValueError("the support-aware policy needs each source's routed gate values")
+                _, h2_cov, evidence = build_expert_hessians(x, p["gates"], h, global_h13=self.global_h13,
+                                                            global_h2=torch.eye(inter, device=dev), device=dev)
+                self.h2_evidence[p["expert"]] = evidence
+                h2, count2 = p["ex"].transform_h2(h2_cov), 1
+            else:
+                h2, count2 = p["ex"].transform_h2(gemm.gram_(torch.zeros((inter, inter), device=dev), h)), p["n"]
             del h, x
             shared = make_shared_h(inter, dev, h2)
-            shared["count"] = p["n"]
+            shared["count"] = count2
             weights.append(p["c"][2].T.contiguous())
             hs.append(shared)
             qas_d.append([self.quant_args("w2")])

@@ -188,6 +188,15 @@ H308 = high_rate_mode()
 K2 = pure_k2_mode()
 _ALL_MODES = (*RATE_TRANSFER_MODES, H308, K2)
 
+# Phase-1 covariance policy of the expert encode (reference qsrt/qsrt.py:220-233): H13 is the layer's
+# global input covariance (local weight 0); H2 is the expert's decoded post-activation covariance shrunk
+# toward its trace-scaled identity by weighted OAS, its local weight capped at 0.75.  Offline encoder
+# controls: they consume no format bits.
+PHASE1_H13_EXPERT_LOCAL_ALPHA = 0.0
+PHASE1_H2_EXPERT_LOCAL_ALPHA = 0.75
+PHASE1_H2_LOCAL_BASIS = "decoded_candidate_post_situ"
+PHASE1_H2_SHRINKAGE_POLICY = "weighted_oas_scaled_identity"
+
 
 def modes_for(geometry: Geometry) -> dict[str, ModeSpec]:
     """The named modes that exist for a geometry (H308 needs 24 records)."""
