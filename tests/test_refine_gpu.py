@@ -1,0 +1,205 @@
+"""Dense-H path refinement on the device (``qsrt_amd.h2_viterbi_refine``,
+reference ``qsrt/h2_viterbi_refine.py``) against the CPU oracle
+(``oracle/refine.py``, pinned by the conditional-target identity and brute
+force in ``tests/test_refine_oracle.py``).
+
+The device run goes through ``quantize_qsrt`` with
+``h2_viterbi_refine_sweeps``; the refinement's inputs are captured on the
+way in and handed to the oracle, which re-runs the sweeps with the C
+Viterbi.  Bar: the refined payload equal state for state, the reconstruction
+equal bit for bit, every sweep's accepted count equal, objectives within
+1e-9 relative, and no sweep raising the objective."""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import bench
+from oracle import fmt as ofmt
+from oracle import refine as oref
+from oracle import tables as otables
+from oracle import viterbi as oviterbi
+from qsrt_amd import exl3_encoder_backend as be
+from qsrt_amd import h2_viterbi_refine as hr
+from qsrt_amd.gradient_guided_viterbi import LowRankViterbiGradientGuidance, ViterbiGradientGuidance
+from qsrt_amd.ldlq import make_shared_h
+from qsrt_amd.sqg_e4m3 import sqg_xor_cheb_t12_bytes
+from qsrt_amd.transform_seeds import default_qsrt_transform_seeds
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _say(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def _config1_gate():
+    d = bench.config_expert(1, torch.device("cpu"))
+    x = d["x"].double()
+    return d["w_gate"].T.contiguous(), (x.T @ x).float(), x.shape[0]
+
+
+def _quant_args(bits: int, seeds, **extra) -> dict:
+    qa = {"K": bits, "seed": seeds.input_sign, "sv_seed": seeds.output_sign, "sigma_reg": 0.01,
+          "devices": [str(DEV)], "apply_out_scales": False, "tailbite_context": 128,
+          "sqg_e4m3_lut": sqg_xor_cheb_t12_bytes(bits)}
+    qa.update(extra)
+    return qa
+
+
+def _encode_capturing(monkeypatch, W, H_sum, count, qa):
+    """``quantize_qsrt`` with the refinement's inputs and result recorded."""
+
+    seen = {}
+    real = hr.refine_h2_viterbi_paths
+
+    def recording(weight, hessian, weight_q, encoded, quantize, config, **kw):
+        seen["inputs"] = (weight.cpu().double().numpy(), hessian.cpu().double().numpy(), weight_q.cpu().numpy(),
+                          encoded.cpu().numpy().view(np.uint16), config)
+        out = real(weight, hessian, weight_q, encoded, quantize, config, **kw)
+        seen["result"] = out
+        return out
+
+    monkeypatch.setattr(hr, "refine_h2_viterbi_paths", recording)
+    shared = make_shared_h(W.shape[0], DEV, H_sum)
+    shared["count"] = count
+    weight_q, proxy, tensors = be.quantize_qsrt(W.to(DEV).clone(), shared, qa, True)
+    torch.cuda.synchronize()
+    monkeypatch.undo()
+    return weight_q, proxy, tensors, seen
+
+
+def _oracle_quantizer(bits: int):
+    """The C Viterbi at the boundary rule the tile operator picks for the
+    T12 tables (the K2 fast rule, the penultimate step otherwise)."""
+
+    labels = otables.t12_values(bits)
+    lag = 0 if bits == 2 else 1
+    return lambda tiles: oviterbi.encode(tiles, labels, K=bits, boundary_lag=lag)
+
+
+def _compare(name, seen, bits, **oracle_kw):
+    W, H, Q0, S0, config = seen["inputs"]
+    res = seen["result"]
+    cpu = oref.refine(W, H, Q0, S0, _oracle_quantizer(bits), sweeps=config.sweeps,
+                      alternate=config.alternate_sweep_order, dither_scales=config.dither_scales,
+                      patterns=config.num_dither_patterns, seed=config.seed, abs_tol=config.acceptance_abs_tol,
+                      rel_tol=config.acceptance_rel_tol, **oracle_kw)
+    g_states = res.encoded.cpu().numpy().view(np.uint16)
+    g_q = res.weight_q.cpu().numpy()
+    differ = int(np.count_nonzero((g_states != cpu["states"]).any(axis=-1)))
+    g_acc = [s.accepted_tiles for s in res.sweep_stats]
+    c_acc = [s["accepted"] for s in cpu["sweeps"]]
+    _say(f"[refine] {name}: accepted per sweep GPU {g_acc} CPU {c_acc}; objective "
+         f"{[round(s.objective_before, 6) for s in res.sweep_stats]} -> {res.sweep_stats[-1].objective_after:.6f} "
+         f"(CPU {cpu['sweeps'][-1]['after']:.6f}); {differ} of {g_states.shape[0] * g_states.shape[1]} tiles differ")
+    assert differ == 0, f"{name}: {differ} refined tiles differ from the CPU refinement"
+    assert np.array_equal(g_q, cpu["Q"])
+    assert g_acc == c_acc
+    for s, c in zip(res.sweep_stats, cpu["sweeps"]):
+        assert s.objective_after <= s.objective_before + max(1e-5, 1e-6 * abs(s.objective_before))
+        assert abs(s.objective_after - c["after"]) <= 1e-9 * abs(c["after"])
+    return res, cpu
+
+
+def test_refinement_matches_cpu_oracle_through_quantize_qsrt(monkeypatch):
+    """Config-1 gate at K2 under H13, two sweeps: the device sweeps equal
+    the oracle's, improve the objective, and the packed payload decodes to
+    the returned reconstruction."""
+
+    W, H_sum, count = _config1_gate()
+    seeds = default_qsrt_transform_seeds(1, "w1")
+    _, proxy0, _ = be.quantize_qsrt(W.to(DEV).clone(), dict(make_shared_h(W.shape[0], DEV, H_sum), count=count),
+                                    _quant_args(2, seeds), False)
+    qa = _quant_args(2, seeds, h2_viterbi_refine_sweeps=2)
+    weight_q, proxy, tensors, seen = _encode_capturing(monkeypatch, W, H_sum, count, qa)
+    res, cpu = _compare("config 1 w1 K2, 2 sweeps", seen, 2)
+    receipt = qa["h2_viterbi_refine_receipt"]
+    assert receipt["enabled"] and receipt["rate_bits"] == 2 and len(receipt["sweeps"]) == len(res.sweep_stats)
+    assert res.sweep_stats[0].accepted_tiles > 0
+    _say(f"[refine] proxy {proxy0:.6f} -> {proxy:.6f}")
+    assert proxy < proxy0
+    # the packed payload is the refined states
+    trellis = tensors["trellis"].cpu().numpy().view(np.uint16)
+    states = ofmt.cyclic_states(ofmt.unpack_symbols(trellis, 2), 2)
+    assert np.array_equal(states, res.encoded.cpu().numpy().view(np.uint16))
+
+
+def test_dithered_refinement_matches_cpu_oracle(monkeypatch):
+    """Two dither scales x two H-whitened patterns (9 proposals per tile):
+    equal to the oracle, and the dithered proposals change the outcome
+    against an undithered refinement of the same start."""
+
+    W, H_sum, count = _config1_gate()
+    qa = _quant_args(2, default_qsrt_transform_seeds(1, "w1"), h2_viterbi_refine_sweeps=2,
+                     h2_viterbi_refine_dither_scales=(0.02, 0.05), h2_viterbi_refine_patterns=2)
+    _, _, _, seen = _encode_capturing(monkeypatch, W, H_sum, count, qa)
+    res, _ = _compare("config 1 w1 K2, dithered", seen, 2)
+    assert res.sweep_stats[0].unique_candidate_paths > res.sweep_stats[0].proposed_tiles
+    Wr, H, Q0, S0, _ = seen["inputs"]
+    plain = hr.refine_h2_viterbi_paths(torch.from_numpy(Wr).to(DEV), torch.from_numpy(H).to(DEV),
+                                       torch.from_numpy(Q0).to(DEV), torch.from_numpy(S0.view(np.int16)).to(DEV),
+                                       lambda t: be.quantize_tiles_multigpu(t, dict(qa)),
+                                       hr.H2ViterbiRefineConfig(sweeps=2))
+    _say(f"[refine] dithered objective {res.sweep_stats[-1].objective_after:.6f}, "
+         f"undithered {plain.sweep_stats[-1].objective_after:.6f}")
+    assert not torch.equal(plain.encoded, res.encoded)
+
+
+@pytest.mark.parametrize("low_rank", [False, True])
+def test_guided_refinement_matches_cpu_oracle(monkeypatch, low_rank):
+    """A linear objective (dense or low-rank gradient) shifts the targets; the
+    guided objective never rises and the sweeps equal the oracle's."""
+
+    W, H_sum, count = _config1_gate()
+    qa = _quant_args(3, default_qsrt_transform_seeds(1, "w1"), h2_viterbi_refine_sweeps=1)
+    _, _, _, seen = _encode_capturing(monkeypatch, W, H_sum, count, qa)
+    Wr, H, Q0, S0, config = seen["inputs"]
+    rng = np.random.default_rng(21)
+    k, n = Wr.shape
+    if low_rank:
+        left, right = rng.standard_normal((k, 4)) * 0.02, rng.standard_normal((4, n)) * 0.02
+        grad = left @ right
+        guidance = LowRankViterbiGradientGuidance(torch.from_numpy(left).to(DEV), torch.from_numpy(right).to(DEV),
+                                                  torch.from_numpy(Q0).to(DEV), "anchor", "kl", strength=0.5)
+    else:
+        grad = rng.standard_normal((k, n)) * 1e-3
+        guidance = ViterbiGradientGuidance(torch.from_numpy(grad).to(DEV), torch.from_numpy(Q0).to(DEV), "anchor",
+                                           "kl", strength=0.5)
+    res = hr.refine_h2_viterbi_paths(torch.from_numpy(Wr).to(DEV), torch.from_numpy(H).to(DEV),
+                                     torch.from_numpy(Q0).to(DEV), torch.from_numpy(S0.view(np.int16)).to(DEV),
+                                     lambda t: be.quantize_tiles_multigpu(t, dict(qa)),
+                                     hr.H2ViterbiRefineConfig(sweeps=2), guidance=guidance)
+    seen["result"] = res
+    seen["inputs"] = (Wr, H, Q0, S0, hr.H2ViterbiRefineConfig(sweeps=2))
+    _compare(f"config 1 w1 K3, {'low-rank' if low_rank else 'dense'} guidance", seen, 3, grad=grad,
+             anchor=Q0.astype(np.float64), strength=0.5)
+    q, lin, tot = hr.dense_h_guided_objective(torch.from_numpy(Wr).to(DEV), res.weight_q,
+                                              torch.from_numpy(H).to(DEV), guidance)
+    assert abs(tot - res.sweep_stats[-1].objective_after) <= 1e-9 * abs(tot)
+
+
+def test_refinement_argument_rules(monkeypatch):
+    W, H_sum, count = _config1_gate()
+    seeds = default_qsrt_transform_seeds(1, "w1")
+    shared = dict(make_shared_h(W.shape[0], DEV, H_sum), count=count)
+    qa = _quant_args(3, seeds, h2_viterbi_refine_sweeps=1, mixed_rate_axis="n",
+                     mixed_tile_bits=[3] * 16 + [4] * 16)
+    with pytest.raises(ValueError, match="uniform rate map"):
+        be.quantize_qsrt(W.to(DEV).clone(), shared, qa, False)
+    # a rate map with one rate is refined at that rate
+    qa = _quant_args(3, seeds, h2_viterbi_refine_sweeps=1, mixed_rate_axis="n", mixed_tile_bits=[4] * 32)
+    be.quantize_qsrt(W.to(DEV).clone(), dict(make_shared_h(W.shape[0], DEV, H_sum), count=count), qa, False)
+    assert qa["h2_viterbi_refine_receipt"]["rate_bits"] == 4
+    with pytest.raises(ValueError, match="sweeps must be positive"):
+        hr.refine_h2_viterbi_paths(W.double().to(DEV), torch.eye(256, device=DEV), W.to(DEV),
+                                   torch.zeros((16, 32, 256), dtype=torch.int16, device=DEV), None,
+                                   hr.H2ViterbiRefineConfig(sweeps=0))
+    with pytest.raises(ValueError, match="tile grid"):
+        hr.refine_h2_viterbi_paths(W.double().to(DEV), torch.eye(256, device=DEV), W.to(DEV),
+                                   torch.zeros((16, 16, 256), dtype=torch.int16, device=DEV), None)
