@@ -544,7 +544,7 @@ def layer_decode(mats: list, reps: int = 3) -> dict:
         "workload": f"the stored config-5 layer read back from its layer file: {n_mat} packed matrices "
                     f"({n_mat // 3} experts x gate, up, down), records {LAYER_RECORD_BITS.count(3)} K3 + "
                     f"{LAYER_RECORD_BITS.count(4)} K4 ({bpw:.3f} trellis bpw) -> bf16",
-        "kernel": "decode_kernel (one launch per rate)",
+        "kernel": "decode_block_wave_kernel (one launch per rate)",
         "ms": round(t * 1e3, 3),
         "G_weights_per_s": round(weights / t / 1e9, 2),
         "roofline": {

@@ -1,8 +1,6 @@
 // Fused trellis decode: packed EXL words -> cyclic states -> E4M3 labels ->
-// W = diag(su) . H128 X H128 . diag(sv) -> bf16 (or f32), one 128x128 block
-// per workgroup iteration.  Each workgroup walks a contiguous run of blocks
-// (runs differ by at most one block); the block cursor advances by carries,
-// with no per-block division.
+// W = diag(su) . H128 X H128 . diag(sv) -> bf16 (or f32), one 128 x 128
+// block at a time.
 //
 // Reference semantics (qsrt/exl3_reference.py:61-302, qsrt/qsrt.py:1175-1209):
 //   X[K, N]  = labels of the states, tile-major, tensor-core order in a tile
@@ -13,36 +11,33 @@
 // and H128 = H8 (x) H16 (Kronecker over the 8x8 tiles of a block and the
 // 16x16 positions of a tile).
 //
-// Per workgroup (8 waves, two workgroups per CU), per block:
-//  A. wave w decodes tile-column w.  Lane (c = lane % 16, g = lane / 16)
-//     takes, in every tile, the 4 values of column c at rows 2g + {0,1,8,9}:
-//     trellis positions 32 (c % 8) + 8 g + 4 (c / 8) + 0..3 (tensor-core
-//     order), one 16 + 3K-bit window of the tile's MSB-first bitstream (EXL
-//     stores adjacent 16-bit words swapped, so a little-endian u32 read is the
-//     big-endian 32-bit chunk of the stream).  Labels come from the
-//     state-indexed E4M3 LUT in LDS; the lane's 32 labels of the tile-column
-//     (8 tiles x 4 rows) are written to a 16 KB LDS label area.
-//  B. wave w produces output tile-row w.  For each tile-column a', the whole
-//     left transform (H8 (x) H16 over the 128 rows) is ONE fp8 MFMA
-//     (16x16x128): A = the lane's 32 labels of that tile-column, B = +-1 with
-//     B[(a, row)][col] = H8[w][a] H16[row][col].  Exact for |label| <= 6 (sums
-//     of at most 128 x 6 on multiples of 2^-9).  The eight results of the
-//     tile-row stay in registers; the right H8 across tile-columns runs on
-//     VALU (exact: < 2^22 units of 2^-9).  Each value is split into fp16
-//     hi + lo (exact, 11 + 11 bits: hi by rounding, lo by a mixed-precision
-//     fma), and the right H16 is two accumulating f16 MFMAs (16x16x16) per
-//     tile, on hi then lo, sharing A = H16 with row i scaled by the fp16 sv
-//     of output column i.  Finally times su/128, conversion, four
-//     consecutive outputs per lane per tile.
-//  Memory traffic is shaped for the vector-memory pipe: a wave's 8 tiles of
-//  packed words arrive with one 16-byte load per lane and are staged through
-//  the wave's own slice of the LDS label area; outputs are staged through the
-//  same slice (XOR-swizzled 16-byte chunks) so each store instruction writes
-//  full 128-byte row segments.  Words, su and sv of the next block are loaded
-//  before this block's stores (vector-memory counters retire in issue order,
-//  so a load issued after a store would wait for the store to drain).
-// Tables whose labels exceed 6 in magnitude use FP32 MFMAs for both products
-// (labels widened exactly to FP32), with the same data movement.
+// Labels: lane (c = lane % 16, g = lane / 16) takes, in a tile, the 4
+// values of column c at rows 2g + {0,1,8,9}: trellis positions 32 (c % 8) +
+// 8 g + 4 (c / 8) + 0..3 (tensor-core order), one 16 + 3K-bit window of the
+// tile's MSB-first bitstream (EXL stores adjacent 16-bit words swapped, so a
+// little-endian u32 read is the big-endian 32-bit chunk of the stream); the
+// labels come from the state-indexed E4M3 LUT in LDS.  A tile-column's words
+// arrive with one 16-byte load per lane and are staged through LDS.
+//
+// decode_block_wave_kernel (tables with |label| <= 6: the T12 tables): one
+// wave per block, twelve waves per CU; see the kernel.  The left transform of
+// a tile is one fp8 MFMA (16x16x128) over the 128 rows of its column, exact
+// for |label| <= 6 (sums of at most 128 x 6 on multiples of 2^-9); the right
+// H8 across tile-columns runs on VALU (exact: < 2^22 units of 2^-9); each
+// value is split into fp16 hi + lo (exact, 11 + 11 bits: hi by rounding, lo by
+// a mixed-precision fma) and the right H16 is two accumulating f16 MFMAs
+// (16x16x16) per tile, on hi then lo, sharing A = H16 with row i scaled by the
+// fp16 sv of output column i; then times su/128 and the conversion.
+//
+// decode_fp32_kernel (tables with larger labels): one workgroup of 8 waves
+// per block, two per CU.  Wave w decodes tile-column w into a 16 KB LDS
+// label area, then produces output tile-row w with FP32 MFMAs for both
+// products (labels widened exactly to FP32).
+//
+// Both stage outputs through LDS (XOR-swizzled 16-byte chunks) so each store
+// instruction writes full 128-byte row segments, and both issue the next
+// block's loads before this block's stores: vector-memory counters retire in
+// issue order, so a load issued after stores returns only once they drain.
 
 #include <algorithm>
 #include <mutex>
@@ -85,12 +80,16 @@ struct Cursor {
     int j, br, bc;
 };
 
+// Cursor of block `blk`: binary search over the jobs' block prefix.
 __device__ __forceinline__ Cursor cursor_at(const Job* jobs, int n_jobs, int64_t blk) {
-    int j = 0;
-    while (j + 1 < n_jobs && jobs[j + 1].first_block <= blk) ++j;
-    const int64_t local = blk - jobs[j].first_block;
-    const int br = static_cast<int>(local / jobs[j].nbc);
-    return Cursor{j, br, static_cast<int>(local - static_cast<int64_t>(br) * jobs[j].nbc)};
+    int lo = 0, hi = n_jobs - 1;  // jobs[lo].first_block <= blk < jobs[hi + 1].first_block
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (jobs[mid].first_block <= blk) lo = mid; else hi = mid - 1;
+    }
+    const int64_t local = blk - jobs[lo].first_block;
+    const int br = static_cast<int>(local / jobs[lo].nbc);
+    return Cursor{lo, br, static_cast<int>(local - static_cast<int64_t>(br) * jobs[lo].nbc)};
 }
 
 __device__ __forceinline__ void cursor_next(const Job* jobs, Cursor& cu) {
@@ -153,9 +152,9 @@ __device__ __forceinline__ uint32_t residual_pair(uint32_t hi, float e0, float e
     return __builtin_bit_cast(uint32_t, lo);
 }
 
-template <int K, bool FP8, typename OutT>
+template <int K, typename OutT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
-void decode_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t total_blocks, const uint8_t* __restrict__ lut) {
+void decode_fp32_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t total_blocks, const uint8_t* __restrict__ lut) {
     static_assert(sizeof(OutT) == 2 || sizeof(OutT) == 4, "bf16 or f32 output");
     __shared__ __attribute__((aligned(16))) uint8_t lut_s[65536];
     // Label area, 2 KB per wave.  During B1: labels of tile-column a', lane l,
@@ -178,38 +177,14 @@ void decode_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t total_block
     const int g = lane >> 4;
     const int rho[4] = {2 * g, 2 * g + 1, 2 * g + 8, 2 * g + 9};
 
-    // Left-product B operand (fp8 +-1): byte j <-> tile-row j / 4, row rho(j % 4); value H8[w][j/4] H16[rho][c].
-    i32x8 bl;
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-        uint32_t v = 0;
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const int j = 4 * r + b;
-            const int s = hsign(w, j >> 2) * hsign(rho[j & 3], c);
-            v |= (s > 0 ? 0x38u : 0xB8u) << (8 * b);  // E4M3 +1 / -1
-        }
-        bl[r] = static_cast<int>(v);
-    }
-    // Right-product A operand rows: H16[c][4g + q]
+    // Right-product A operand rows: H16[c][4g + q]; left-product operand: H16[rho(i)][c]
     float hr[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) hr[q] = static_cast<float>(hsign(c, 4 * g + q));
-    float hl[4];  // FP32 path: H16[rho(i)][c]
+    float hl[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) hl[i] = static_cast<float>(hsign(rho[i], c));
-    // fp16 sign masks of H16[c][4g + q], q = 0..3, as two packed pairs
-    uint32_t hsg[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-        hsg[h] = (hr[2 * h] < 0.f ? 0x8000u : 0u) | (hr[2 * h + 1] < 0.f ? 0x80000000u : 0u);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) asm volatile("" : "+v"(hsg[h]));
-    float neg_one = -1.0f;
-    asm volatile("" : "+v"(neg_one));
     // Keep the operand constants in registers instead of recomputing them in the loop.
-#pragma unroll
-    for (int r = 0; r < 8; ++r) asm volatile("" : "+v"(bl[r]));
 #pragma unroll
     for (int q = 0; q < 4; ++q) asm volatile("" : "+v"(hr[q]));
 
@@ -237,10 +212,7 @@ void decode_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t total_block
     __syncthreads();
 
     for (int64_t blk = begin; blk < end; ++blk) {
-        // ---- A: stage the tile-column's words, decode the lane's labels.  From here to the end of B1 the wave
-        // runs at raised issue priority and drops back for B2: a wave in its right product and stores then
-        // yields issue slots to waves still gathering labels or in the left product, so the two workgroups'
-        // phases overlap better (bit-identical output; 0.82-0.86 ms against 0.89-0.96 ms on 96 K3 matrices).
+        // ---- A: stage the tile-column's words, decode the lane's labels (raised issue priority through B1)
         __builtin_amdgcn_s_setprio(2);
         if (lane < 16 * K) reinterpret_cast<u32x4*>(slice)[lane] = words;
         uint32_t lab[8];
@@ -256,15 +228,9 @@ void decode_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t total_block
         lab_w[0] = make_uint4(lab[0], lab[1], lab[2], lab[3]);
         lab_w[64] = make_uint4(lab[4], lab[5], lab[6], lab[7]);
         // this block's scale operands, before the prefetch below replaces su and sv
-        uint32_t sv2[8];  // FP8 path: fp16 pairs
-        float svf[8];     // FP32 path
+        float svf[8];
 #pragma unroll
-        for (int a = 0; a < 8; ++a) {
-            if constexpr (FP8)
-                sv2[a] = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(sv[a]), static_cast<_Float16>(sv[a])});
-            else
-                svf[a] = sv[a];
-        }
+        for (int a = 0; a < 8; ++a) svf[a] = sv[a];
         const float su_cur = su;
         const BlockCtx cur = ctx;
         // ---- prefetch the next block (before this block's stores)
@@ -284,22 +250,14 @@ void decode_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t total_block
         for (int a2 = 0; a2 < 8; ++a2) {
             const uint4 x0 = lab_r[(a2 * 2) * 64], x1 = lab_r[(a2 * 2 + 1) * 64];
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            if constexpr (FP8) {
-                const i32x8 av = {static_cast<int>(x0.x), static_cast<int>(x0.y), static_cast<int>(x0.z),
-                                  static_cast<int>(x0.w), static_cast<int>(x1.x), static_cast<int>(x1.y),
-                                  static_cast<int>(x1.z), static_cast<int>(x1.w)};
-                // format 0 = E4M3 for A and B; E8M0 scales 127 = 1.0
-                acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bl, acc, 0, 0, 0, 127, 0, 127);
-            } else {
-                const uint32_t words8[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            const uint32_t words8[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-                for (int a = 0; a < 8; ++a) {
-                    const float sgn = static_cast<float>(hsign(w, a));
+            for (int a = 0; a < 8; ++a) {
+                const float sgn = static_cast<float>(hsign(w, a));
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float x = sgn * qsrt::e4m3_to_float((words8[a] >> (8 * i)) & 0xFFu);
-                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x, hl[i], acc, 0, 0, 0);
-                    }
+                for (int i = 0; i < 4; ++i) {
+                    const float x = sgn * qsrt::e4m3_to_float((words8[a] >> (8 * i)) & 0xFFu);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x, hl[i], acc, 0, 0, 0);
                 }
             }
             e[a2] = acc;
@@ -307,7 +265,7 @@ void decode_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t total_block
         __syncthreads();  // every wave is done reading labels: slices are private again
         __builtin_amdgcn_s_setprio(0);
 
-        // ---- B2: right H8 across tile-columns (exact on the fp8 path)
+        // ---- B2: right H8 across tile-columns
 #pragma unroll
         for (int h = 1; h < 8; h <<= 1) {
 #pragma unroll
@@ -330,29 +288,8 @@ void decode_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t total_block
             for (int t = 0; t < kTilesPerRound; ++t) {
                 const int a = rd * kTilesPerRound + t;
                 f32x4 d = {0.f, 0.f, 0.f, 0.f};
-                if constexpr (FP8) {
-                    // exact split: hi = e rounded to fp16 (11 significant bits), lo = e - hi, formed by a
-                    // mixed-precision fma straight into fp16.  e is a multiple of 2^-9 below 2^13, so
-                    // |lo| <= ulp(hi) / 2 is a multiple of 2^-9 with at most 11 significant bits: exact.
-                    uint32_t hi01 = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(e[a][0]),
-                                                                              static_cast<_Float16>(e[a][1])});
-                    uint32_t hi23 = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(e[a][2]),
-                                                                              static_cast<_Float16>(e[a][3])});
-                    asm volatile("" : "+v"(hi01), "+v"(hi23));
-                    typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
-                    const u32x2v hraw = {hi01, hi23};
-                    const u32x2v lraw = {residual_pair(hi01, e[a][0], e[a][1], neg_one), residual_pair(hi23, e[a][2], e[a][3], neg_one)};
-                    // A rows: +-sv of the output column (sign bits from H16 via XOR), shared by the hi and lo
-                    // products (k = the lane group's four columns 4 g .. 4 g + 3)
-                    const u32x2v araw = {sv2[a] ^ hsg[0], sv2[a] ^ hsg[1]};
-                    const f16x4 avh = __builtin_bit_cast(f16x4, araw);
-                    d = __builtin_amdgcn_mfma_f32_16x16x16f16(avh, __builtin_bit_cast(f16x4, hraw), d, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x16f16(avh, __builtin_bit_cast(f16x4, lraw), d, 0, 0, 0);
-                } else {
 #pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        d = __builtin_amdgcn_mfma_f32_16x16x4f32(hr[q] * svf[a], e[a][q], d, 0, 0, 0);
-                }
+                for (int q = 0; q < 4; ++q) d = __builtin_amdgcn_mfma_f32_16x16x4f32(hr[q] * svf[a], e[a][q], d, 0, 0, 0);
                 d = d * su_cur;
                 // row c, staged columns 16 t + 4 g .. +3 -> byte offset, 16-byte chunks XOR-swizzled by row
                 const int byte = (16 * t + 4 * g) * static_cast<int>(sizeof(OutT));
@@ -379,16 +316,282 @@ void decode_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t total_block
     }
 }
 
+// ---------------------------------------------------------------------------
+// One wave per block.  Each wave owns whole 128 x 128 blocks: it decodes all
+// 64 tiles' labels straight into registers -- lane (c, g) holds, for every
+// tile-column a', the 32 labels that are the left product's A operand of
+// that column (64 VGPRs) -- and then produces the block's eight output
+// tile-rows one after another: for tile-row r, eight fp8 MFMAs (one per
+// tile-column, B = H8[r][.] (x) H16 in E4M3 +-1), the right H8 across the
+// eight results on VALU, the right H16 as two f16 MFMAs per tile on the exact
+// hi/lo split, times su/128, bf16 or f32, staged through the wave's 4 KB LDS
+// slice into full 128-byte row segments.  Successive tile-rows are visited in
+// Gray-code order, so B changes by one sign flip on four of its eight
+// registers between them.  Nothing is shared between waves but the LUT: no
+// label exchange and no barrier after the LUT load, so the workgroup's twelve
+// waves drift into different phases (gathers, MFMAs, VALU, stores) and keep
+// every pipe busy at once.
+constexpr int kBlockWaves = 12;  // one workgroup of 12 waves per CU (3 per SIMD)
+constexpr int kBlockThreads = 64 * kBlockWaves;
+constexpr int kSliceBytes = 2048;  // half an output tile-row of bf16 (16 rows x 128 B); a tile-column's words
+constexpr int kScaleBytes = 1024;  // a block's su (128 f32) and fp16-paired sv (128 x 2 fp16)
+
+
+// Wave-uniform values computed on the vector unit, moved to scalar registers
+// (the block context would otherwise hold 32 VGPRs across the label phase).
+__device__ __forceinline__ int64_t sgpr64(int64_t v) {
+    const uint64_t u = static_cast<uint64_t>(v);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+template <typename T>
+__device__ __forceinline__ T* sgpr_ptr(T* p) {
+    return reinterpret_cast<T*>(sgpr64(reinterpret_cast<int64_t>(p)));
+}
+__device__ __forceinline__ BlockCtx uniform_ctx(BlockCtx x) {
+    x.words = sgpr_ptr(x.words);
+    x.trs = sgpr64(x.trs);
+    x.tcs = sgpr64(x.tcs);
+    x.su = sgpr_ptr(x.su);
+    x.sv = sgpr_ptr(x.sv);
+    x.out = sgpr_ptr(x.out);
+    x.ld = sgpr64(x.ld);
+    return x;
+}
+
+template <int K, typename OutT>
+__global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(3, 3)))
+void decode_block_wave_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t total_blocks,
+                              const uint8_t* __restrict__ lut) {
+    static_assert(sizeof(OutT) == 2 || sizeof(OutT) == 4, "bf16 or f32 output");
+    __shared__ __attribute__((aligned(16))) uint8_t lut_s[65536];
+    __shared__ __attribute__((aligned(16))) uint8_t slices[kBlockWaves * kSliceBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t scales[kBlockWaves * kScaleBytes];
+
+    for (int i = threadIdx.x; i < 65536 / 16; i += kBlockThreads)
+        reinterpret_cast<uint4*>(lut_s)[i] = reinterpret_cast<const uint4*>(lut)[i];
+    __syncthreads();  // the kernel's only barrier
+
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t gw = static_cast<int64_t>(blockIdx.x) * kBlockWaves + w;
+    const int64_t nw = static_cast<int64_t>(gridDim.x) * kBlockWaves;
+    const int64_t begin = sgpr64(total_blocks * gw / nw);
+    const int64_t end = sgpr64(total_blocks * (gw + 1) / nw);
+    if (begin >= end) return;
+
+    const int c = lane & 15;
+    const int g = lane >> 4;
+    const int rho[4] = {2 * g, 2 * g + 1, 2 * g + 8, 2 * g + 9};
+    // B of tile-row 0: byte i of every register is H16[rho(i)][c] in E4M3 (+1 0x38, -1 0xB8)
+    uint32_t bbase = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bbase |= (hsign(rho[i], c) > 0 ? 0x38u : 0xB8u) << (8 * i);
+    uint32_t hsg[2];  // fp16 sign masks of H16[c][4g + q], q = 0..3, as two packed pairs
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+        hsg[h] = (hsign(c, 4 * g + 2 * h) < 0 ? 0x8000u : 0u) | (hsign(c, 4 * g + 2 * h + 1) < 0 ? 0x80000000u : 0u);
+    float neg_one = -1.0f;
+    asm volatile("" : "+v"(neg_one));
+
+    const int p0 = 32 * (c & 7) + 8 * g + 4 * (c >> 3);
+    int b0 = (p0 + 1) * K - 16;
+    if (b0 < 0) b0 += 256 * K;
+    const int m0 = b0 >> 5;
+    const int m1 = (m0 + 1) % (8 * K);
+    const uint32_t rsh = 32u - static_cast<uint32_t>(b0 & 31);
+
+    uint8_t* slice = slices + kSliceBytes * w;
+    const uint32_t* wstage = reinterpret_cast<const uint32_t*>(slice);
+    float* su_s = reinterpret_cast<float*>(scales + kScaleBytes * w);  // [128] row scales
+    uint32_t* sv_s = reinterpret_cast<uint32_t*>(su_s + 128);          // [8][16]: sv of column 16 a + c, fp16 pair
+
+    // Loads of a block are issued before the previous block's stores: vector-memory counters retire in issue
+    // order, so a load issued after stores returns only once they have drained.
+    Cursor cu = cursor_at(jobs, n_jobs, begin);
+    BlockCtx ctx = uniform_ctx(block_ctx(jobs, cu, sizeof(OutT)));
+    u32x4 words[8];
+#pragma unroll
+    for (int col = 0; col < 8; ++col) words[col] = fetch_words<K>(ctx, col, lane);
+    float su_n[8], sv_n[8];
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+        su_n[a] = ((gf32)ctx.su)[16 * a + c];
+        sv_n[a] = ((gf32)ctx.sv)[16 * a + c];
+    }
+
+    for (int64_t blk = begin; blk < end; ++blk) {
+        const BlockCtx cur = ctx;
+        // ---- labels of all 64 tiles, tile-column by tile-column (high issue priority: the gathers are the
+        // phase other waves' MFMA and store phases can hide behind)
+        __builtin_amdgcn_s_setprio(2);
+        i32x8 av[8];
+#pragma unroll
+        for (int col = 0; col < 8; ++col) {
+            if (lane < 16 * K) reinterpret_cast<u32x4*>(slice)[lane] = words[col];
+            words[col] = u32x4{0u, 0u, 0u, 0u};  // dead until the next block's prefetch (not held across it)
+            uint32_t lab[8];
+#pragma unroll
+            for (int a = 0; a < 8; ++a) {
+                const uint32_t lo = wstage[a * 8 * K + m0], hi = wstage[a * 8 * K + m1];
+                const uint32_t win = __builtin_amdgcn_alignbit(lo, hi, rsh);  // stream bits [b0, b0 + 32)
+                const uint32_t v01 = lut_s[win >> 16] | (static_cast<uint32_t>(lut_s[(win >> (16 - K)) & 0xFFFFu]) << 16);
+                const uint32_t v23 = lut_s[(win >> (16 - 2 * K)) & 0xFFFFu] |
+                                     (static_cast<uint32_t>(lut_s[(win >> (16 - 3 * K)) & 0xFFFFu]) << 16);
+                lab[a] = __builtin_amdgcn_perm(v23, v01, 0x06040200u);
+            }
+            // pack the column's labels here (its 32 gathers in flight together), not after all 256 gathers
+#pragma unroll
+            for (int a = 0; a < 8; ++a) {
+                asm volatile("" : "+v"(lab[a]));
+                av[col][a] = static_cast<int>(lab[a]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // this block's scales into the wave's LDS scale area (lanes of one c write the same values), then the
+        // next block's loads, all before this block's first store
+#pragma unroll
+        for (int a = 0; a < 8; ++a) {
+            su_s[16 * a + c] = su_n[a];
+            sv_s[16 * a + c] =
+                __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(sv_n[a]), static_cast<_Float16>(sv_n[a])});
+        }
+        const bool more = blk + 1 < end;
+#pragma unroll
+        for (int a = 0; a < 8; ++a) su_n[a] = sv_n[a] = 0.f;  // likewise
+        if (more) {
+            cursor_next(jobs, cu);
+            ctx = uniform_ctx(block_ctx(jobs, cu, sizeof(OutT)));
+#pragma unroll
+            for (int a = 0; a < 8; ++a) {
+                su_n[a] = ((gf32)ctx.su)[16 * a + c];
+                sv_n[a] = ((gf32)ctx.sv)[16 * a + c];
+            }
+        }
+        // ---- output tile-rows in Gray-code order; the left MFMAs at priority 1, the rest at 0
+        uint32_t bb = bbase;
+        asm volatile("" : "+v"(bb));  // eight copies per block, not eight registers held across it
+        i32x8 bl;
+#pragma unroll
+        for (int a = 0; a < 8; ++a) bl[a] = static_cast<int>(bb);
+        auto tile_row = [&](const int step, const bool last) {
+            const int r = step ^ (step >> 1);
+            const float su_r = su_s[16 * r + c];
+            if (step > 0) {
+                const int m = __builtin_ctz(step);  // the bit of r that changed: H8[r][a] flips where a has it
+#pragma unroll
+                for (int a = 0; a < 8; ++a)
+                    bl[a] = static_cast<int>(static_cast<uint32_t>(bl[a]) ^ (((a >> m) & 1) ? 0x80808080u : 0u));
+            }
+            __builtin_amdgcn_s_setprio(1);
+            f32x4 e[8];
+#pragma unroll
+            for (int a2 = 0; a2 < 8; ++a2) {
+                const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+                e[a2] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[a2], bl, zero, 0, 0, 0, 127, 0, 127);
+            }
+            // the labels are dead after the last tile-row's left products: the next block's words take their
+            // registers, loaded before this tile-row's stores (only earlier tile-rows' stores are ahead of them)
+            if (last && more) {
+                __builtin_amdgcn_sched_barrier(0);  // not above the MFMAs that still read the labels
+#pragma unroll
+                for (int col = 0; col < 8; ++col) words[col] = fetch_words<K>(ctx, col, lane);
+            }
+            __builtin_amdgcn_s_setprio(0);
+            // right H8 across tile-columns (exact)
+#pragma unroll
+            for (int h = 1; h < 8; h <<= 1) {
+#pragma unroll
+                for (int a = 0; a < 8; ++a) {
+                    if (a & h) continue;
+                    const f32x4 x = e[a], y = e[a + h];
+                    e[a] = x + y;
+                    e[a + h] = x - y;
+                }
+            }
+            constexpr int kRowBytes = 128;
+            constexpr int kChunks = kRowBytes / 16;
+            constexpr int kTilesPerRound = kRowBytes / (16 * static_cast<int>(sizeof(OutT)));
+            constexpr int kRounds = 8 / kTilesPerRound;
+            char* out_row0 = cur.out + (16 * r) * cur.ld * sizeof(OutT);
+#pragma unroll
+            for (int rd = 0; rd < kRounds; ++rd) {
+#pragma unroll
+                for (int t = 0; t < kTilesPerRound; ++t) {
+                    const int a = rd * kTilesPerRound + t;
+                    uint32_t hi01 = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(e[a][0]),
+                                                                              static_cast<_Float16>(e[a][1])});
+                    uint32_t hi23 = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(e[a][2]),
+                                                                              static_cast<_Float16>(e[a][3])});
+                    asm volatile("" : "+v"(hi01), "+v"(hi23));
+                    typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+                    const u32x2v hraw = {hi01, hi23};
+                    const u32x2v lraw = {residual_pair(hi01, e[a][0], e[a][1], neg_one),
+                                         residual_pair(hi23, e[a][2], e[a][3], neg_one)};
+                    const uint32_t sv2 = sv_s[16 * a + c];
+                    const u32x2v araw = {sv2 ^ hsg[0], sv2 ^ hsg[1]};
+                    const f16x4 avh = __builtin_bit_cast(f16x4, araw);
+                    f32x4 d = {0.f, 0.f, 0.f, 0.f};
+                    d = __builtin_amdgcn_mfma_f32_16x16x16f16(avh, __builtin_bit_cast(f16x4, hraw), d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x16f16(avh, __builtin_bit_cast(f16x4, lraw), d, 0, 0, 0);
+                    d = d * su_r;
+                    const int byte = (16 * t + 4 * g) * static_cast<int>(sizeof(OutT));
+                    const int chunk = (byte >> 4) ^ (c & (kChunks - 1));
+                    char* dst = reinterpret_cast<char*>(slice) + c * kRowBytes + chunk * 16 + (byte & 15);
+                    if constexpr (sizeof(OutT) == 2) {
+                        typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+                        const bf16x4 o = {static_cast<__bf16>(d[0]), static_cast<__bf16>(d[1]),
+                                          static_cast<__bf16>(d[2]), static_cast<__bf16>(d[3])};
+                        *reinterpret_cast<bf16x4*>(dst) = o;
+                    } else {
+                        *reinterpret_cast<f32x4*>(dst) = d;
+                    }
+                }
+#pragma unroll
+                for (int r0 = 0; r0 < 16; r0 += 64 / kChunks) {
+                    const int row = r0 + lane / kChunks, chunk = lane % kChunks;
+                    const u32x4 v =
+                        *reinterpret_cast<const u32x4*>(slice + row * kRowBytes + ((chunk ^ (row & (kChunks - 1))) * 16));
+                    char* dst = out_row0 + row * cur.ld * sizeof(OutT) + rd * kRowBytes + chunk * 16;
+                    *(__attribute__((address_space(1))) u32x4*)dst = v;
+                }
+            }
+        };
+#pragma unroll 1
+        for (int step = 0; step < 7; ++step) tile_row(step, false);
+        tile_row(7, true);  // peeled: the labels die inside it, which makes room for the next block's words
+    }
+}
+
+// One workgroup of kBlockWaves waves per CU (fewer when there are fewer blocks).
+template <int K>
+void launch_block_wave_k(const Job* jobs, int n_jobs, int64_t total, const uint8_t* lut, int out_dtype, int cus,
+                         hipStream_t stream) {
+    const int64_t groups = (total + kBlockWaves - 1) / kBlockWaves;
+    const unsigned grid = static_cast<unsigned>(std::min<int64_t>(cus, groups));
+    if (out_dtype == 0)
+        hipLaunchKernelGGL((decode_block_wave_kernel<K, __bf16>), dim3(grid), dim3(kBlockThreads), 0, stream, jobs,
+                           n_jobs, total, lut);
+    else
+        hipLaunchKernelGGL((decode_block_wave_kernel<K, float>), dim3(grid), dim3(kBlockThreads), 0, stream, jobs,
+                           n_jobs, total, lut);
+}
+
 template <int K, bool FP8>
 void launch(const Job* jobs, int n_jobs, int64_t total, const uint8_t* lut, int out_dtype, int cus,
             hipStream_t stream) {
-    const unsigned grid = static_cast<unsigned>(std::min<int64_t>(2 * static_cast<int64_t>(cus), total));  // 2 per CU
-    if (out_dtype == 0)
-        hipLaunchKernelGGL((decode_kernel<K, FP8, __bf16>), dim3(grid), dim3(kThreads), 0, stream, jobs, n_jobs, total,
-                           lut);
-    else
-        hipLaunchKernelGGL((decode_kernel<K, FP8, float>), dim3(grid), dim3(kThreads), 0, stream, jobs, n_jobs, total,
-                           lut);
+    if constexpr (FP8) {
+        launch_block_wave_k<K>(jobs, n_jobs, total, lut, out_dtype, cus, stream);
+    } else {
+        const unsigned grid = static_cast<unsigned>(std::min<int64_t>(2 * static_cast<int64_t>(cus), total));  // 2 per CU
+        if (out_dtype == 0)
+            hipLaunchKernelGGL((decode_fp32_kernel<K, __bf16>), dim3(grid), dim3(kThreads), 0, stream, jobs, n_jobs,
+                               total, lut);
+        else
+            hipLaunchKernelGGL((decode_fp32_kernel<K, float>), dim3(grid), dim3(kThreads), 0, stream, jobs, n_jobs,
+                               total, lut);
+    }
 }
 
 // Job-table upload by kernel argument: the host validates and converts up to
@@ -396,12 +599,14 @@ void launch(const Job* jobs, int n_jobs, int64_t total, const uint8_t* lut, int 
 // to the device table.  Arguments are captured when the launch is enqueued,
 // so there is no host buffer whose lifetime must outlast an asynchronous
 // copy, no allocation, and the upload is stream-ordered like any launch.
-constexpr int kUploadChunk = 16;
+constexpr int kUploadChunk = 44;  // 44 x 88-byte jobs: one launch's 4 KiB argument block
 
 struct JobChunk {
     Job jobs[kUploadChunk];
     int count;
 };
+
+static_assert(sizeof(Job) == 88 && sizeof(JobChunk) <= 4096, "a job chunk must fit one kernel argument block");
 
 __global__ __launch_bounds__(64) void upload_jobs_kernel(JobChunk chunk, Job* __restrict__ dst) {
     const int i = static_cast<int>(threadIdx.x);

@@ -160,9 +160,17 @@ def test_quantize_qsrt_output_hessian():
         _encode(W, H, _qa(bits, output_hessian=h_out, h2_viterbi_refine_sweeps=1), False)
 
 
-def test_dense_h_refinement_sweeps_raise():
+def test_dense_h_refinement_sweeps_run_one_sided():
+    """Refinement sweeps run on the one-sided encode (the two-sided
+    combination is rejected above) and report an enabled receipt whose
+    objective never rises."""
+
     k, n, bits = 256, 128, 2
     H = _ar1_gram(k, 0.9, 4096, 21) * 4096
     W = torch.from_numpy((np.random.default_rng(22).standard_normal((k, n)) * 0.02).astype(np.float32)).to(DEV)
-    with pytest.raises(NotImplementedError, match="research control"):
-        _encode(W, H, _qa(bits, h2_viterbi_refine_sweeps=2), False)
+    qa = _qa(bits, h2_viterbi_refine_sweeps=2)
+    _encode(W, H, qa, False)
+    receipt = qa["h2_viterbi_refine_receipt"]
+    assert receipt["enabled"] and receipt["rate_bits"] == bits
+    for sweep in receipt["sweeps"]:
+        assert sweep["objective_after"] <= sweep["objective_before"] * (1 + 1e-9)
