@@ -60,8 +60,8 @@ VITERBI_VALU_ISSUE_FRAC_PMC = {"K2": 1.06, "K3": 0.94}
 # on a 4 GiB device copy; K3/K4 over every dispatch of a 20-expert layer step, K2 from the microbench;
 # profiles/layer_encode_config5.md): mostly the traceback decision stream.
 VITERBI_HBM_BYTES_PER_TILE = {2: 1.631e6, 3: 1.633e6, 4: 0.816e6}
-# Same counters for the decode launches: 1.013 x their algorithmic bytes (profiles/decode_kernel_layer.md).
-DECODE_TRAFFIC_OVER_ALGORITHMIC = 1.013
+# Same counters for the decode launches: 1.10 x their algorithmic bytes (profiles/decode_kernel_layer.md).
+DECODE_TRAFFIC_OVER_ALGORITHMIC = 1.102
 # Same counters at the bench's GEMM and Hadamard shapes (profiles/gemm_tn_kernels_expert_shapes.md,
 # profiles/hadamard_kernel_expert_matrix.md): HBM bytes per launch (the Hessian capture: its main kernel and
 # the fixup kernel of its K-split tiles together).
@@ -70,6 +70,11 @@ HADAMARD_HBM_BYTES = {"left": 1.1782e8, "right": 1.1765e8}
 # Same counters for the BaKron top band's left + right launches (profiles/bakron_band_kernels_config4_gate.md):
 # mostly the right product's re-reads of the input factor.
 BAKRON_TOP_BAND_HBM_BYTES = 5.515e9
+
+# Every `traffic` field is a profile constant (HBM bytes per launch from a rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+# pass of this file's own command, calibrated on a device copy), not a counter read by this run.
+TRAFFIC_NOTE = ("HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes ({}), scaled by the "
+                "same counters on a device copy; a profile constant, not measured in this run")
 
 LAYER_EXPERTS = 384
 LAYER_TOKENS = 65536
@@ -458,7 +463,51 @@ def layer_bench(steps: int, warmup: int, experts: int = LAYER_EXPERTS):
     proxies = [e[m]["proxy"] for e in encoded for m in ("w1", "w3", "w2")]
     del sources
     return {"wall": wall, "steps": steps, "experts": experts, "step_s": step_s, "weights": weights, "viterbi": vit, "encoded": encoded,
+            "first_step_experts": bounds[1],
             "proxy_mean": sum(proxies) / len(proxies), "proxy_max": max(proxies), "warm": warm, "counts": counts}
+
+
+def layer_streamed(lay: dict) -> dict:
+    """BASELINE's "work is streamed from host", measured on the layer's first
+    step: the same experts with their bf16 gate/up/down and routed
+    calibration rows in pinned host memory, uploaded to HBM inside the timed
+    region, then encoded exactly as the resident step was.  The upload is
+    not overlapped with the encode (a side-stream upload of step i + 1 during
+    step i would hide it); the line reports its share."""
+
+    dev = torch.device("cuda:0")
+    n = lay["first_step_experts"]
+    host = []
+    for e in range(n):
+        src = expert_source(5, dev, expert=e, tokens=lay["counts"][e])
+        host.append({"expert": src["expert"], "tokens": src["tokens"],
+                     "w": tuple(t.cpu().pin_memory() for t in src["w"]), "x": src["x"].cpu().pin_memory(),
+                     "gates": src["gates"].cpu().pin_memory()})
+        del src
+    torch.cuda.synchronize()
+    nbytes = sum(t.numel() * t.element_size() for h in host for t in (*h["w"], h["x"], h["gates"]))
+    enc = ExpertEncoder(dev, hidden=LAYER_HIDDEN, inter=LAYER_INTER, record_bits=LAYER_RECORD_BITS,
+                        scope=("bench-streamed", LAYER_ID))
+    from qsrt_amd import exl3_encoder_backend as be
+    for key in [k for k in be._SHARED_INPUT_SCALES if k[0] == enc.scope]:
+        del be._SHARED_INPUT_SCALES[key]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    srcs = [{"expert": h["expert"], "tokens": h["tokens"], "w": tuple(t.to(dev, non_blocking=True) for t in h["w"]),
+             "x": h["x"].to(dev, non_blocking=True), "gates": h["gates"].to(dev, non_blocking=True)} for h in host]
+    torch.cuda.synchronize()
+    upload = time.perf_counter() - t0
+    for b0 in range(0, n, MAX_BATCH_EXPERTS):
+        enc.encode(srcs[b0:b0 + MAX_BATCH_EXPERTS])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    weights = n * 3 * LAYER_HIDDEN * LAYER_INTER
+    resident = lay["step_s"][0]
+    return {"workload": f"the layer's first step ({n} experts) with its sources in pinned host memory, uploaded inside "
+                        "the timed region, then encoded",
+            "M_weights_per_s": round(weights / wall / 1e6, 3), "seconds": round(wall, 3),
+            "upload_seconds": round(upload, 4), "upload_bytes": nbytes, "upload_GB_per_s": round(nbytes / upload / 1e9, 2),
+            "resident_seconds": round(resident, 3), "resident_M_weights_per_s": round(weights / resident / 1e6, 3)}
 
 
 def layer_store(encoded: list, directory: str) -> dict:
@@ -550,6 +599,7 @@ def layer_decode(mats: list, reps: int = 3) -> dict:
         "roofline": {
             "bound": "hbm", "achieved": round(byts / t / 1e9, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
             "frac": round(byts / t / 1e9 / HBM_PEAK_GBPS, 4), "traffic": round(byts * DECODE_TRAFFIC_OVER_ALGORITHMIC),
+            "traffic_note": TRAFFIC_NOTE.format("profiles/decode_kernel_layer.md"),
             "algorithmic": f"{bpw:.3f}/8 B payload + 2 B bf16 out per weight + (K + N) f32 scales per matrix "
                            f"= {byts:.4g} B per layer (both launches)",
         },
@@ -559,6 +609,19 @@ def layer_decode(mats: list, reps: int = 3) -> dict:
 # ---------------------------------------------------------------------------
 # CPU baseline and parity on a sample of the layer
 # ---------------------------------------------------------------------------
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (``/proc/cpuinfo``, what ``lscpu`` prints)."""
+
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def _sign_draw(n: int, seed: int):
@@ -631,6 +694,7 @@ def layer_cpu_sample(first: dict, source: dict, blocks: int = 96) -> dict:
 
     return {
         "cpu": {"value": round(n_w / t_rec / 1e6, 5), "unit": "M weights/s", "cores": threads, "kind": "port",
+                "model": cpu_model(),
                 "sample": f"expert 0 w1 of the layer ({source['tokens']} routed rows), the bottom {blocks} of {kt} "
                           f"16-row blocks ({blocks * nt} tiles, {n_w} weights): the float64 BlockLDLQ of "
                           f"oracle/encode.py with oracle/viterbi_ref.c (AVX2) on {threads} OpenMP threads at the "
@@ -745,7 +809,8 @@ def microbench_cpu(bits: int = 3, seconds: float = 6.0) -> dict:
         ov.encode(tiles, lab, K=bits, boundary_lag=1, threads=threads)
         n += len(tiles)
     per_tile = (time.perf_counter() - t0) / n
-    return {"value": round(256 / per_tile / 1e6, 4), "unit": "M weights/s", "cores": threads, "ms_per_tile": per_tile * 1e3,
+    return {"value": round(256 / per_tile / 1e6, 4), "unit": "M weights/s", "cores": threads, "model": cpu_model(),
+            "ms_per_tile": per_tile * 1e3,
             "sample": f"{n} microbench tiles at K{bits}, oracle/viterbi_ref.c (AVX2) with {threads} OpenMP threads"}
 
 
@@ -886,6 +951,7 @@ def gemm_bench(steps: int = 20):
         return {"kernel": name, "shape": shape, "ms": round(ms, 4), "roofline": {
             "bound": "mfma", "achieved": round(t, 1), "peak": MFMA_PEAK_TFLOPS[dtype], "unit": "TFLOP/s",
             "frac": round(t / MFMA_PEAK_TFLOPS[dtype], 4), "traffic": round(GEMM_HBM_BYTES[key]),
+            "traffic_note": TRAFFIC_NOTE.format("profiles/gemm_tn_kernels_expert_shapes.md"),
             "algorithmic": f"{what} = {fl:.4g} flops/launch ({dtype} in, f32 accumulate)"}}
 
     return {
@@ -916,6 +982,7 @@ def hadamard_bench(steps: int = 5):
         out[side] = {"kernel": "hadamard_kernel", "ms": round(ms, 4), "roofline": {
             "bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
             "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": round(HADAMARD_HBM_BYTES[side]),
+            "traffic_note": TRAFFIC_NOTE.format("profiles/hadamard_kernel_expert_matrix.md"),
             "algorithmic": f"8 B/element x {k * n} elements/launch"}}
     del W
     torch.cuda.empty_cache()
@@ -1009,6 +1076,7 @@ def bakron_bench(steps: int = 5):
             "top_band": {"diagonals": list(top), "ms": round(top_ms, 4), "roofline": {
                 "bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "traffic": round(BAKRON_TOP_BAND_HBM_BYTES),
+                "traffic_note": TRAFFIC_NOTE.format("profiles/bakron_band_kernels_config4_gate.md"),
                 "algorithmic": f"2 x 16^3 flops per (target, source) block pair x {top_flops // 8192} pairs"},
                 "block_lower": {"ms": round(lower_ms, 4),
                                 "tflops": round(lower_flops / (lower_ms / 1e3) / 1e12, 2),
@@ -1077,6 +1145,7 @@ def headline(lay: dict, warmup: int) -> dict:
             "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
             "traffic": round(sum(VITERBI_HBM_BYTES_PER_TILE[int(k[1:])] * d["tiles"] for k, d in vit["by_rate"].items())
                              / max(vit["launches"], 1)),
+            "traffic_note": TRAFFIC_NOTE.format("profiles/layer_encode_config5.md"),
             "kernel": "viterbi_tiles_kernel",
             "algorithmic": f"{FLOPS_PER_EDGE} FP32 flops/edge x {int(EDGES_PER_WEIGHT)} edges/weight x 256 weights/tile "
                            f"x {mean_tiles:.1f} tiles/launch (mean over {vit['launches']} launches in the timed region)",
@@ -1153,6 +1222,10 @@ def main() -> int:
             log(f"[bench] CPU {cs['cpu']['value']} M w/s on {cs['cpu']['cores']} threads; "
                 f"parity {json.dumps(cs['parity'])}")
         del first, sample_src
+        if not args.no_secondary:
+            log("[bench] layer step streamed from host")
+            result["streamed_from_host"] = layer_streamed(lay)
+            log(f"[bench] streamed {json.dumps(result['streamed_from_host'])}")
     else:
         result = {"metric": "encoded weights/sec (M/s) at K=2/3 on one GPU", "value": None,
                   "note": f"headline not run (--only {args.only})"}

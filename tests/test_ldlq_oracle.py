@@ -66,6 +66,26 @@ def test_backend_block_ldl_retries_indefinite_hessian():
     assert float(H_used[0, 0]) > float(H[0, 0])  # damping was added
 
 
+def test_backend_block_ldl_factors_in_float64_without_the_fp32_retry():
+    """The factorisation runs in float64: a Hessian whose FP32 Cholesky fails
+    but whose float64 one succeeds (rank 16 of 64 plus 2e-7 relative
+    damping) is factored as given, with no extra damping.  The reference's
+    FP32 factorisation would have retried with 2 sigma_reg mean(diag)
+    (qsrt/exl3_encoder_backend.py:331-351); the retry here fires only for a
+    matrix that is indefinite in float64 (previous test)."""
+
+    g = torch.Generator().manual_seed(5)
+    A = torch.randn(64, 16, generator=g, dtype=torch.float64)
+    H64 = A @ A.T
+    H = (H64 + 2e-7 * H64.diagonal().mean() * torch.eye(64, dtype=torch.float64)).float()
+    assert int(torch.linalg.cholesky_ex(H)[1]) > 0  # FP32 Cholesky fails ...
+    assert int(torch.linalg.cholesky_ex(H.double())[1]) == 0  # ... float64 succeeds
+    L, H_used = be.block_ldl(H.clone(), 16, {"sigma_reg": 0.025}, False)
+    assert torch.equal(H_used, H)  # no damping was added
+    L_ref, _ = oldlq.block_ldl(H.double().numpy(), 16)
+    assert np.allclose(L.double().numpy(), L_ref, rtol=1e-3, atol=1e-3)
+
+
 def test_backend_hessian_finalisation_matches_oracle_congruence():
     k = 256
     H = torch.from_numpy(_spd(k, 5)).float()
