@@ -53,7 +53,7 @@ FLOPS_PER_EDGE = 3  # d = label - x (1), fma(d, d, cost) (2)
 FP32_PEAK_TFLOPS = 157.3
 FP32_UNPACKED_PEAK_TFLOPS = 78.6  # 256 CUs x 64 FP32 FMA lanes x 2 flops x 2.4 GHz, no packed FP32
 HBM_PEAK_GBPS = 8000.0
-MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "f32": 157.3}
+MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "f32": 157.3, "f64": 78.6}
 # VALU issue-slot occupancy of viterbi_tiles_kernel by PMC (profiles/viterbi_tiles_kernel_microbench.md)
 VITERBI_VALU_ISSUE_FRAC_PMC = {"K2": 1.06, "K3": 0.94}
 # HBM bytes per tile of the Viterbi kernel by rate (FETCH_SIZE x 2.00 + WRITE_SIZE x 1.00 per dispatch, calibrated
@@ -921,10 +921,12 @@ def k2_expert_bench(reps: int = 2) -> dict:
 
 
 def gemm_bench(steps: int = 20):
-    """The two MFMA GEMM shapes of the config-4 expert encode:
-    Hessian capture ``H += X^T X`` of 16,384 bf16 tokens x 7168 channels,
-    and one LDLQ span update ``P[:begin] += L[span, :begin]^T (W - Q)[span]``
-    (M = 7040, K = 128, N = 2048, FP32)."""
+    """The MFMA GEMM shapes of the config-4 expert encode: Hessian capture
+    ``H += X^T X`` of 16,384 bf16 tokens x 7168 channels, and one LDLQ span
+    update ``P[:begin] += L[span, :begin]^T (W - Q)[span]`` (M = 7040,
+    K = 128, N = 2048) on the float64 matrix cores as the encoder runs it
+    (float64 L, W and P, FP32 Q) and, for the two-sided recursion's FP32
+    contract, on the FP32 ones."""
 
     from qsrt_amd import gemm
 
@@ -943,22 +945,29 @@ def gemm_bench(steps: int = 20):
     P = torch.zeros((m, nn), device=dev)
     ms_l = _time_ms(lambda: gemm.addmm_sub_tn_(P, L, W, Q), steps)
     fl_l = 2.0 * m * kk * nn
-    del L, W, Q, P
+    L64, W64, P64 = L.double(), W.double(), P.double()
+    ms_l64 = _time_ms(lambda: gemm.addmm_sub_tn_(P64, L64, W64, Q), steps)
+    del L, W, Q, P, L64, W64, P64
     torch.cuda.empty_cache()
 
     def line(key, name, ms, fl, dtype, shape, what):
         t = fl / (ms / 1e3) / 1e12
+        acc = "f64" if dtype == "f64" else "f32"
+        traffic = GEMM_HBM_BYTES.get(key)
         return {"kernel": name, "shape": shape, "ms": round(ms, 4), "roofline": {
             "bound": "mfma", "achieved": round(t, 1), "peak": MFMA_PEAK_TFLOPS[dtype], "unit": "TFLOP/s",
-            "frac": round(t / MFMA_PEAK_TFLOPS[dtype], 4), "traffic": round(GEMM_HBM_BYTES[key]),
-            "traffic_note": TRAFFIC_NOTE.format("profiles/gemm_tn_kernels_expert_shapes.md"),
-            "algorithmic": f"{what} = {fl:.4g} flops/launch ({dtype} in, f32 accumulate)"}}
+            "frac": round(t / MFMA_PEAK_TFLOPS[dtype], 4), "traffic": None if traffic is None else round(traffic),
+            "traffic_note": (TRAFFIC_NOTE.format("profiles/gemm_tn_kernels_expert_shapes.md") if traffic is not None
+                             else "not profiled"),
+            "algorithmic": f"{what} = {fl:.4g} flops/launch ({dtype} in, {acc} accumulate)"}}
 
     return {
         "hessian_capture": line("hessian_capture", "gemm_tn_bf16_kernel", ms_h, fl_h, "bf16",
                                 f"X [{n} x {k}] bf16 -> H [{k} x {k}] f32", "n k (k + 1) (symmetric)"),
-        "ldlq_span_update": line("ldlq_span_update", "gemm_tn_f32_kernel", ms_l, fl_l, "f32",
-                                 f"L^T [{m} x {kk}] (W - Q) [{kk} x {nn}] f32", "2 M N K"),
+        "ldlq_span_update": line("ldlq_span_update_f64", "gemm_tn_f64_kernel", ms_l64, fl_l, "f64",
+                                 f"L^T [{m} x {kk}] (W - Q) [{kk} x {nn}] f64 (Q f32)", "2 M N K"),
+        "ldlq_span_update_f32": line("ldlq_span_update", "gemm_tn_f32_kernel", ms_l, fl_l, "f32",
+                                     f"L^T [{m} x {kk}] (W - Q) [{kk} x {nn}] f32", "2 M N K"),
     }
 
 

@@ -203,3 +203,18 @@ def test_refinement_argument_rules(monkeypatch):
     with pytest.raises(ValueError, match="tile grid"):
         hr.refine_h2_viterbi_paths(W.double().to(DEV), torch.eye(256, device=DEV), W.to(DEV),
                                    torch.zeros((16, 16, 256), dtype=torch.int16, device=DEV), None)
+
+
+def test_full_size_refinement_matches_cpu_oracle(monkeypatch):
+    """BASELINE config 4 at full size: the 7168 x 2048 gate at K2 (448 row
+    blocks, 57,344 tiles) under H13 of 16,384 rows, one sweep: the device
+    sweep equals the oracle's tile for tile."""
+
+    d = bench.config_expert(4, DEV)
+    xd = d["x"].double()
+    H_sum = (xd.T @ xd).float().cpu()
+    del xd
+    qa = _quant_args(2, default_qsrt_transform_seeds(1, "w1"), h2_viterbi_refine_sweeps=1)
+    _, _, _, seen = _encode_capturing(monkeypatch, d["w_gate"].T.contiguous().cpu(), H_sum, d["x"].shape[0], qa)
+    res, _ = _compare("config 4 gate (full size) K2, 1 sweep", seen, 2)
+    assert res.sweep_stats[0].accepted_tiles > 0
