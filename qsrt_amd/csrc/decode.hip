@@ -23,11 +23,14 @@
 // wave per block, twelve waves per CU; see the kernel.  The left transform of
 // a tile is one fp8 MFMA (16x16x128) over the 128 rows of its column, exact
 // for |label| <= 6 (sums of at most 128 x 6 on multiples of 2^-9); the right
-// H8 across tile-columns runs on VALU (exact: < 2^22 units of 2^-9); each
-// value is split into fp16 hi + lo (exact, 11 + 11 bits: hi by rounding, lo by
-// a mixed-precision fma) and the right H16 is two accumulating f16 MFMAs
-// (16x16x16) per tile, on hi then lo, sharing A = H16 with row i scaled by the
-// fp16 sv of output column i; then times su/128 and the conversion.
+// H8 = H2 (x) H4 across tile-columns: its two stages over tile-column bits 1
+// and 2 run on VALU (exact: < 2^22 units of 2^-9); each value is split into
+// fp16 hi + lo (exact, 11 + 11 bits: hi by rounding, lo by a mixed-precision
+// fma); the stage over bit 0 and the right H16 are two accumulating f16 MFMAs
+// (16x16x32) per output tile, on hi then lo of the tile-column pair (2p,
+// 2p + 1), with A = H16 with row i scaled by the fp16 sv of output column i,
+// repeated over the pair with the sign of H2; then times su/128 and the
+// conversion.
 //
 // decode_fp32_kernel (tables with larger labels): one workgroup of 8 waves
 // per block, two per CU.  Wave w decodes tile-column w into a 16 KB LDS
@@ -137,6 +140,7 @@ __device__ __forceinline__ u32x4 fetch_words(const BlockCtx& x, int w, int lane)
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 // fp16 pair {e0 - hi.x, e1 - hi.y} with hi a packed fp16 pair: each value is
 // one mixed-precision fma (fp16 source, fp32 addend, result rounded once to
@@ -322,10 +326,11 @@ void decode_fp32_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t total_
 // tile-column a', the 32 labels that are the left product's A operand of
 // that column (64 VGPRs) -- and then produces the block's eight output
 // tile-rows one after another: for tile-row r, eight fp8 MFMAs (one per
-// tile-column, B = H8[r][.] (x) H16 in E4M3 +-1), the right H8 across the
-// eight results on VALU, the right H16 as two f16 MFMAs per tile on the exact
-// hi/lo split, times su/128, bf16 or f32, staged through the wave's 4 KB LDS
-// slice into full 128-byte row segments.  Successive tile-rows are visited in
+// tile-column, B = H8[r][.] (x) H16 in E4M3 +-1), the right H8's stages over
+// tile-column bits 1 and 2 on VALU, its stage over bit 0 with the right H16 as
+// two f16 MFMAs (K = 32) per tile on the exact hi/lo split of a tile-column
+// pair, times su/128, bf16 or f32, staged through the wave's 2 KB LDS slice
+// into full 128-byte row segments.  Successive tile-rows are visited in
 // Gray-code order, so B changes by one sign flip on four of its eight
 // registers between them.  Nothing is shared between waves but the LUT: no
 // label exchange and no barrier after the LUT load, so the workgroup's twelve
@@ -499,9 +504,9 @@ void decode_block_wave_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t 
                 for (int col = 0; col < 8; ++col) words[col] = fetch_words<K>(ctx, col, lane);
             }
             __builtin_amdgcn_s_setprio(0);
-            // right H8 across tile-columns (exact)
+            // right H8 over tile-column bits 1 and 2 (exact); bit 0 runs inside the right MFMAs
 #pragma unroll
-            for (int h = 1; h < 8; h <<= 1) {
+            for (int h = 2; h < 8; h <<= 1) {
 #pragma unroll
                 for (int a = 0; a < 8; ++a) {
                     if (a & h) continue;
@@ -518,34 +523,48 @@ void decode_block_wave_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t 
 #pragma unroll
             for (int rd = 0; rd < kRounds; ++rd) {
 #pragma unroll
-                for (int t = 0; t < kTilesPerRound; ++t) {
-                    const int a = rd * kTilesPerRound + t;
-                    uint32_t hi01 = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(e[a][0]),
-                                                                              static_cast<_Float16>(e[a][1])});
-                    uint32_t hi23 = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(e[a][2]),
-                                                                              static_cast<_Float16>(e[a][3])});
-                    asm volatile("" : "+v"(hi01), "+v"(hi23));
-                    typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
-                    const u32x2v hraw = {hi01, hi23};
-                    const u32x2v lraw = {residual_pair(hi01, e[a][0], e[a][1], neg_one),
-                                         residual_pair(hi23, e[a][2], e[a][3], neg_one)};
-                    const uint32_t sv2 = sv_s[16 * a + c];
-                    const u32x2v araw = {sv2 ^ hsg[0], sv2 ^ hsg[1]};
-                    const f16x4 avh = __builtin_bit_cast(f16x4, araw);
-                    f32x4 d = {0.f, 0.f, 0.f, 0.f};
-                    d = __builtin_amdgcn_mfma_f32_16x16x16f16(avh, __builtin_bit_cast(f16x4, hraw), d, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x16f16(avh, __builtin_bit_cast(f16x4, lraw), d, 0, 0, 0);
-                    d = d * su_r;
-                    const int byte = (16 * t + 4 * g) * static_cast<int>(sizeof(OutT));
-                    const int chunk = (byte >> 4) ^ (c & (kChunks - 1));
-                    char* dst = reinterpret_cast<char*>(slice) + c * kRowBytes + chunk * 16 + (byte & 15);
-                    if constexpr (sizeof(OutT) == 2) {
-                        typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-                        const bf16x4 o = {static_cast<__bf16>(d[0]), static_cast<__bf16>(d[1]),
-                                          static_cast<__bf16>(d[2]), static_cast<__bf16>(d[3])};
-                        *reinterpret_cast<bf16x4*>(dst) = o;
-                    } else {
-                        *reinterpret_cast<f32x4*>(dst) = d;
+                for (int tp = 0; tp < kTilesPerRound; tp += 2) {
+                    // tile-column pair (2p, 2p + 1) = (a0, a0 + 1): K = 32 slots 0-3 carry a0's values (rows 4g..4g+3
+                    // of the lane's column), slots 4-7 those of a0 + 1; A repeats the H16 row for both, negated on
+                    // slots 4-7 for the odd output tile (H2[1][1] = -1)
+                    const int a0 = rd * kTilesPerRound + tp;
+                    uint32_t hi[4];
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        hi[2 * u] = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(e[a0 + u][0]),
+                                                                      static_cast<_Float16>(e[a0 + u][1])});
+                        hi[2 * u + 1] = __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(e[a0 + u][2]),
+                                                                          static_cast<_Float16>(e[a0 + u][3])});
+                    }
+                    asm volatile("" : "+v"(hi[0]), "+v"(hi[1]), "+v"(hi[2]), "+v"(hi[3]));
+                    const u32x4 hraw = {hi[0], hi[1], hi[2], hi[3]};
+                    const u32x4 lraw = {residual_pair(hi[0], e[a0][0], e[a0][1], neg_one),
+                                        residual_pair(hi[1], e[a0][2], e[a0][3], neg_one),
+                                        residual_pair(hi[2], e[a0 + 1][0], e[a0 + 1][1], neg_one),
+                                        residual_pair(hi[3], e[a0 + 1][2], e[a0 + 1][3], neg_one)};
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const int t = tp + u, a = a0 + u;
+                        const uint32_t sv2 = sv_s[16 * a + c];
+                        const uint32_t x0 = sv2 ^ hsg[0], x1 = sv2 ^ hsg[1];
+                        const uint32_t flip = u ? 0x80008000u : 0u;
+                        const u32x4 araw = {x0, x1, x0 ^ flip, x1 ^ flip};
+                        const f16x8 avh = __builtin_bit_cast(f16x8, araw);
+                        f32x4 d = {0.f, 0.f, 0.f, 0.f};
+                        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(avh, __builtin_bit_cast(f16x8, hraw), d, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(avh, __builtin_bit_cast(f16x8, lraw), d, 0, 0, 0);
+                        d = d * su_r;
+                        const int byte = (16 * t + 4 * g) * static_cast<int>(sizeof(OutT));
+                        const int chunk = (byte >> 4) ^ (c & (kChunks - 1));
+                        char* dst = reinterpret_cast<char*>(slice) + c * kRowBytes + chunk * 16 + (byte & 15);
+                        if constexpr (sizeof(OutT) == 2) {
+                            typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+                            const bf16x4 o = {static_cast<__bf16>(d[0]), static_cast<__bf16>(d[1]),
+                                              static_cast<__bf16>(d[2]), static_cast<__bf16>(d[3])};
+                            *reinterpret_cast<bf16x4*>(dst) = o;
+                        } else {
+                            *reinterpret_cast<f32x4*>(dst) = d;
+                        }
                     }
                 }
 #pragma unroll
