@@ -60,8 +60,8 @@ VITERBI_VALU_ISSUE_FRAC_PMC = {"K2": 1.06, "K3": 0.94}
 # on a 4 GiB device copy; K3/K4 over every dispatch of a 20-expert layer step, K2 from the microbench;
 # profiles/layer_encode_config5.md): mostly the traceback decision stream.
 VITERBI_HBM_BYTES_PER_TILE = {2: 1.631e6, 3: 1.633e6, 4: 0.816e6}
-# Same counters for the decode launches: 1.10 x their algorithmic bytes (profiles/decode_kernel_layer.md).
-DECODE_TRAFFIC_OVER_ALGORITHMIC = 1.102
+# Same counters for the decode launches: 1.03 x their algorithmic bytes (profiles/decode_kernel_layer.md).
+DECODE_TRAFFIC_OVER_ALGORITHMIC = 1.032
 # Same counters at the bench's GEMM and Hadamard shapes (profiles/gemm_tn_kernels_expert_shapes.md,
 # profiles/hadamard_kernel_expert_matrix.md): HBM bytes per launch (the Hessian capture: its main kernel and
 # the fixup kernel of its K-split tiles together).
