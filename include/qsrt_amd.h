@@ -278,6 +278,21 @@ int qsrt_gemm_tn_f64(double *C, const double *A, const double *B, const float *B
                      int64_t lda, int64_t ldb, int64_t ldb2, int64_t ldc, double alpha, void *stream);
 
 /*
+ * qsrt_gemm_tn_f64 over `batch` members in one launch:
+ *   C[b] += alpha * A[b]^T (B[b] - B2[b])    b < batch
+ * with X[b] = X + b * stride_x (elements; even, and stride_c >= (M - 1) * ldc + N
+ * so the members of C do not overlap).  Each member's elements are computed
+ * exactly as qsrt_gemm_tn_f64 computes them.  The batched BlockLDLQ span
+ * product of the mixed and batched recursions, which the reference issues as
+ * one baddbmm over the members: _baddbmm_ldlq(product_cache[:, :begin],
+ * Ls[:, begin:end, :begin]^T, W[:, begin:end] - Q[:, begin:end])
+ * (qsrt/exl3_encoder_backend.py:1170-1187, call :1458-1471).
+ */
+int qsrt_gemm_tn_f64_batched(double *C, const double *A, const double *B, const float *B2, int batch, int64_t M,
+                             int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldb2, int64_t ldc, int64_t stride_c,
+                             int64_t stride_a, int64_t stride_b, int64_t stride_b2, double alpha, void *stream);
+
+/*
  * Diagonal-block step of a blocked float64 Cholesky factorisation, for
  * `batch` matrices A[b] = A + b * batch_stride (n x n, row-major, leading
  * dimension n).  The lower triangle of the nb x nb block at (j0, j0) is

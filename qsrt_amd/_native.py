@@ -71,6 +71,11 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
          ctypes.c_double, _c_void_p],
     ),
+    "qsrt_gemm_tn_f64_batched": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_double, _c_void_p],
+    ),
     "qsrt_chol_diag_block_f64": (
         _c_int, [_c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_void_p, _c_void_p, _c_void_p],
     ),

@@ -675,16 +675,25 @@ __device__ __forceinline__ void store_f64(const F64Chunk& ch, double (*As)[kBM +
 }
 
 // Two waves per SIMD: 128 accumulator registers plus the operand chunk fit in 256.
+// Batch members are consecutive runs of tiles_m * tiles_n workgroups (member-major, so a member's operands stay
+// in L2 while its tiles run); member b reads A + b * sa, B + b * sb, B2 + b * sb2 and updates C + b * sc.
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void gemm_tn_f64_kernel(double* __restrict__ C, const double* __restrict__ A,
                                                                const double* __restrict__ B,
                                                                const float* __restrict__ B2, int64_t M, int64_t N,
                                                                int64_t K, int64_t lda, int64_t ldb, int64_t ldb2,
-                                                               int64_t ldc, double alpha, int64_t tiles_n) {
+                                                               int64_t ldc, double alpha, int64_t tiles_n,
+                                                               int64_t tiles_per_member, int64_t sc, int64_t sa,
+                                                               int64_t sb, int64_t sb2) {
     __shared__ __attribute__((aligned(16))) double As[2][kBK64][kBM + kPad64];
     __shared__ __attribute__((aligned(16))) double Bs[2][kBK64][kBN + kPad64];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int c = lane & 15, g = lane >> 4;
-    const int64_t m0 = (blockIdx.x / tiles_n) * kBM, n0 = (blockIdx.x % tiles_n) * kBN;
+    const int64_t member = blockIdx.x / tiles_per_member, tile = blockIdx.x - member * tiles_per_member;
+    C += member * sc;
+    A += member * sa;
+    B += member * sb;
+    if (B2) B2 += member * sb2;
+    const int64_t m0 = (tile / tiles_n) * kBM, n0 = (tile % tiles_n) * kBN;
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
 
     const bool seed = alpha == 1.0;  // accumulators start from C (plain store at the end)
@@ -754,10 +763,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 
 extern "C" {
 
-int qsrt_gemm_tn_f64(double* C, const double* A, const double* B, const float* B2, int64_t M, int64_t N, int64_t K,
-                     int64_t lda, int64_t ldb, int64_t ldb2, int64_t ldc, double alpha, void* stream_handle) {
-    if (M < 0 || N < 0 || K < 0) return qsrt::fail(qsrt::kBadArgument, "gemm f64: negative extent");
-    if (M == 0 || N == 0 || K == 0) return qsrt::kOk;
+int qsrt_gemm_tn_f64_batched(double* C, const double* A, const double* B, const float* B2, int batch, int64_t M,
+                             int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldb2, int64_t ldc, int64_t stride_c,
+                             int64_t stride_a, int64_t stride_b, int64_t stride_b2, double alpha,
+                             void* stream_handle) {
+    if (batch < 0 || M < 0 || N < 0 || K < 0) return qsrt::fail(qsrt::kBadArgument, "gemm f64: negative extent");
+    if (batch == 0 || M == 0 || N == 0 || K == 0) return qsrt::kOk;
     if (!C || !A || !B) return qsrt::fail(qsrt::kBadArgument, "null pointer argument");
     if (lda < M || ldb < N || ldc < N || (B2 && ldb2 < N))
         return qsrt::fail(qsrt::kBadArgument, "gemm f64: leading dimension smaller than the row");
@@ -765,13 +776,24 @@ int qsrt_gemm_tn_f64(double* C, const double* A, const double* B, const float* B
         reinterpret_cast<uintptr_t>(B) % 16 || (B2 && reinterpret_cast<uintptr_t>(B2) % 8))
         return qsrt::fail(qsrt::kBadArgument,
                           "gemm f64: A and B must be 16-byte aligned, B2 8-byte aligned, leading dimensions even");
+    if (batch > 1 && (stride_a % 2 || stride_b % 2 || (B2 && stride_b2 % 2) || stride_c < 0 || stride_a < 0 ||
+                      stride_b < 0 || stride_b2 < 0))
+        return qsrt::fail(qsrt::kBadArgument, "gemm f64: member strides must be non-negative and even");
+    if (batch > 1 && stride_c < (M - 1) * ldc + N)
+        return qsrt::fail(qsrt::kBadArgument, "gemm f64: members of C overlap (stride_c < (M - 1) * ldc + N)");
     const int64_t tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
-    if (tiles_m * tiles_n > 0x7fffffff) return qsrt::fail(qsrt::kBadArgument, "gemm f64: too many tiles");
-    hipLaunchKernelGGL(gemm_tn_f64_kernel, dim3(static_cast<unsigned>(tiles_m * tiles_n)), dim3(kThreads), 0,
+    if (tiles_m * tiles_n * batch > 0x7fffffff) return qsrt::fail(qsrt::kBadArgument, "gemm f64: too many tiles");
+    hipLaunchKernelGGL(gemm_tn_f64_kernel, dim3(static_cast<unsigned>(tiles_m * tiles_n * batch)), dim3(kThreads), 0,
                        static_cast<hipStream_t>(stream_handle), C, A, B, B2, M, N, K, lda, ldb, ldb2, ldc, alpha,
-                       tiles_n);
+                       tiles_n, tiles_m * tiles_n, batch > 1 ? stride_c : 0, batch > 1 ? stride_a : 0,
+                       batch > 1 ? stride_b : 0, batch > 1 ? stride_b2 : 0);
     QSRT_HIP_TRY(hipGetLastError());
     return qsrt::kOk;
+}
+
+int qsrt_gemm_tn_f64(double* C, const double* A, const double* B, const float* B2, int64_t M, int64_t N, int64_t K,
+                     int64_t lda, int64_t ldb, int64_t ldb2, int64_t ldc, double alpha, void* stream_handle) {
+    return qsrt_gemm_tn_f64_batched(C, A, B, B2, 1, M, N, K, lda, ldb, ldb2, ldc, 0, 0, 0, 0, alpha, stream_handle);
 }
 
 }  // extern "C"

@@ -101,6 +101,49 @@ def _addmm_sub_tn_f64_(C, A, B, B2, alpha):
     return C
 
 
+def baddmm_sub_tn_f64_(C: torch.Tensor, A: torch.Tensor, B: torch.Tensor, B2: torch.Tensor | None = None,
+                       alpha: float = 1.0) -> torch.Tensor:
+    """Per member ``C[b] += alpha * A[b]^T (B[b] - B2[b])`` in one launch on
+    the float64 matrix cores (the batched BlockLDLQ span product; the
+    reference's ``_baddbmm_ldlq``, ``qsrt/exl3_encoder_backend.py:1170-1187``).
+    ``C``, ``A``, ``B`` float64 and ``B2`` float32 (or None), each
+    ``[batch, rows, cols]`` with row-major members at a uniform member
+    stride.  Every element equals what ``addmm_sub_tn_`` computes for its
+    member."""
+
+    if C.dim() != 3 or A.dim() != 3 or B.dim() != 3 or (B2 is not None and B2.dim() != 3):
+        raise ValueError("baddmm_sub_tn_f64_: [batch, rows, cols] operands expected")
+    batch, K, M = A.shape
+    if (B.shape[0] != batch or B.shape[1] != K or C.shape != (batch, M, B.shape[2])
+            or (B2 is not None and B2.shape != B.shape)):
+        raise ValueError("baddmm_sub_tn_f64_: incompatible shapes")
+    if A.dtype != torch.float64 or B.dtype != torch.float64 or C.dtype != torch.float64 or (
+            B2 is not None and B2.dtype != torch.float32):
+        raise ValueError("baddmm_sub_tn_f64_: float64 C, A, B and a float32 B2 expected")
+    if not C.is_cuda:
+        rhs = B if B2 is None else B - B2.to(B.dtype)
+        return C.baddbmm_(A.transpose(1, 2), rhs, alpha=alpha)
+    N = B.shape[2]
+
+    def members_ok(t, align):
+        return (t.stride(2) == 1 and t.stride(1) % 2 == 0 and t.stride(0) % 2 == 0 and t.data_ptr() % align == 0
+                and t.stride(1) >= t.shape[2])
+
+    if batch <= 1 or not (members_ok(C, 8) and members_ok(A, 16) and members_ok(B, 16)
+                          and (B2 is None or members_ok(B2, 8)) and C.stride(0) >= (M - 1) * C.stride(1) + N):
+        for b in range(batch):
+            addmm_sub_tn_(C[b], A[b], B[b], None if B2 is None else B2[b], alpha=alpha)
+        return C
+    _native.check(
+        _native.lib().qsrt_gemm_tn_f64_batched(
+            C.data_ptr(), A.data_ptr(), B.data_ptr(), None if B2 is None else B2.data_ptr(), batch, M, N, K,
+            A.stride(1), B.stride(1), 0 if B2 is None else B2.stride(1), C.stride(1), C.stride(0), A.stride(0),
+            B.stride(0), 0 if B2 is None else B2.stride(0), float(alpha), _native.stream_handle(C.device)),
+        "qsrt_gemm_tn_f64_batched",
+    )
+    return C
+
+
 def addmm_tn_(C: torch.Tensor, A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
     """``C += A^T @ B`` in FP32."""
 

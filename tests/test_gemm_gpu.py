@@ -239,3 +239,60 @@ def test_float64_span_update_is_width_independent():
     want = P0[:begin].cpu().numpy() + L[begin:end, :begin].cpu().numpy().T @ (
         W[begin:end].cpu().numpy() - Q[begin:end].double().cpu().numpy())
     assert _rel(wide[:begin].cpu().numpy(), want) < 1e-13
+
+
+@pytest.mark.parametrize("batch,k,n,begin,end", [(5, 1024, 2048, 768, 896), (3, 512, 200, 128, 256),
+                                                 (40, 768, 384, 512, 640), (2, 256, 130, 112, 240)])
+def test_float64_batched_span_update_equals_the_member_loop(batch, k, n, begin, end):
+    """qsrt_gemm_tn_f64_batched over the views the recursion passes
+    (prod_cache[:, :begin], Ls[:, begin:end, :begin], W[:, begin:end],
+    Q[:, begin:end]) equals the per-member qsrt_gemm_tn_f64 loop bit for bit,
+    with and without B2 and at a scaled alpha, and equals float64 on the CPU."""
+
+    print(f"[gemm] f64 batched {batch} x [{begin} x {n}] K{end - begin}", file=sys.stderr, flush=True)
+    g = torch.Generator().manual_seed(batch * 7 + k + n)
+    L = torch.randn(batch, k, k, generator=g, dtype=torch.float64).cuda()
+    W = torch.randn(batch, k, n, generator=g, dtype=torch.float64).cuda()
+    Q = torch.randn(batch, k, n, generator=g).cuda()
+    P0 = torch.randn(batch, k, n, generator=g, dtype=torch.float64).cuda()
+    for alpha, q in ((1.0, Q), (-0.5, Q), (1.0, None)):
+        loop = P0.clone()
+        for b in range(batch):
+            gemm.addmm_sub_tn_(loop[b, :begin], L[b, begin:end, :begin], W[b, begin:end],
+                               None if q is None else q[b, begin:end], alpha=alpha)
+        one = P0.clone()
+        gemm.baddmm_sub_tn_f64_(one[:, :begin], L[:, begin:end, :begin], W[:, begin:end],
+                                None if q is None else q[:, begin:end], alpha=alpha)
+        assert torch.equal(one, loop)
+    b = batch - 1
+    want = P0[b, :begin].cpu().numpy() + L[b, begin:end, :begin].cpu().numpy().T @ W[b, begin:end].cpu().numpy()
+    assert _rel(one[b, :begin].cpu().numpy(), want) < 1e-13
+
+
+def test_float64_batched_span_update_argument_rules():
+    """Overlapping members of C and odd member strides are refused by the
+    C-ABI entry point with an error, before any launch; the Python wrapper
+    falls back to the member loop for views the batched kernel cannot take."""
+
+    C = torch.zeros(2, 64, 64, dtype=torch.float64).cuda()
+    A = torch.zeros(2, 16, 64, dtype=torch.float64).cuda()
+    B = torch.zeros(2, 16, 64, dtype=torch.float64).cuda()
+    lib = _native.lib()
+    stream = _native.stream_handle(C.device)
+    # stride_c of 64 elements: member 1 would start on row 1 of member 0
+    rc = lib.qsrt_gemm_tn_f64_batched(C.data_ptr(), A.data_ptr(), B.data_ptr(), None, 2, 64, 64, 16, 64, 64, 0, 64,
+                                      64, 16 * 64, 16 * 64, 0, 1.0, stream)
+    assert rc != 0 and b"overlap" in lib.qsrt_last_error()
+    rc = lib.qsrt_gemm_tn_f64_batched(C.data_ptr(), A.data_ptr(), B.data_ptr(), None, 2, 64, 64, 16, 64, 64, 0, 64,
+                                      64 * 64, 16 * 64 + 1, 16 * 64, 0, 1.0, stream)
+    assert rc != 0 and b"even" in lib.qsrt_last_error()
+    with pytest.raises(ValueError, match="incompatible"):
+        gemm.baddmm_sub_tn_f64_(C, A, B[:, :8])
+    # a column slice of C has members that the kernel could take, a transposed A does not: the loop serves it
+    At = torch.randn(2, 64, 16, dtype=torch.float64).cuda().transpose(1, 2)
+    Bm = torch.randn(2, 16, 64, dtype=torch.float64).cuda()
+    want = C.clone()
+    for b in range(2):
+        want[b] += At[b].T @ Bm[b]
+    gemm.baddmm_sub_tn_f64_(C, At, Bm)
+    assert _rel(C.cpu().numpy(), want.cpu().numpy()) < 1e-13
