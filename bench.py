@@ -65,7 +65,8 @@ DECODE_TRAFFIC_OVER_ALGORITHMIC = 1.032
 # Same counters at the bench's GEMM and Hadamard shapes (profiles/gemm_tn_kernels_expert_shapes.md,
 # profiles/hadamard_kernel_expert_matrix.md): HBM bytes per launch (the Hessian capture: its main kernel and
 # the fixup kernel of its K-split tiles together).
-GEMM_HBM_BYTES = {"hessian_capture": 2.435e9, "ldlq_span_update": 1.485e8, "ldlq_span_update_f64": 2.950e8}
+GEMM_HBM_BYTES = {"hessian_capture": 2.435e9, "ldlq_span_update": 1.485e8, "ldlq_span_update_f64": 2.950e8,
+                  "ldlq_span_update_batched_f64": 6.16e9}
 HADAMARD_HBM_BYTES = {"left": 1.1782e8, "right": 1.1765e8}
 # Same counters for the BaKron top band's left + right launches (profiles/bakron_band_kernels_config4_gate.md):
 # mostly the right product's re-reads of the input factor.
@@ -926,7 +927,8 @@ def gemm_bench(steps: int = 20):
     update ``P[:begin] += L[span, :begin]^T (W - Q)[span]`` (M = 7040,
     K = 128, N = 2048) on the float64 matrix cores as the encoder runs it
     (float64 L, W and P, FP32 Q) and, for the two-sided recursion's FP32
-    contract, on the FP32 ones."""
+    contract, on the FP32 ones; and the layer's batched form (40 members,
+    M = 3584), one launch as the batched recursion issues it."""
 
     from qsrt_amd import gemm
 
@@ -949,6 +951,17 @@ def gemm_bench(steps: int = 20):
     ms_l64 = _time_ms(lambda: gemm.addmm_sub_tn_(P64, L64, W64, Q), steps)
     del L, W, Q, P, L64, W64, P64
     torch.cuda.empty_cache()
+    # the layer's batched span update: the 40 gate/up members of a 20-expert step in one launch, at the
+    # middle of the recursion (M = begin = 3584 rows still to update)
+    nb, mb = 40, 3584
+    Lb = torch.randn((nb, kk, mb), device=dev, generator=g, dtype=torch.float64)
+    Wb = torch.randn((nb, kk, nn), device=dev, generator=g, dtype=torch.float64)
+    Qb = torch.randn((nb, kk, nn), device=dev, generator=g)
+    Pb = torch.zeros((nb, mb, nn), device=dev, dtype=torch.float64)
+    ms_lb = _time_ms(lambda: gemm.baddmm_sub_tn_f64_(Pb, Lb, Wb, Qb), steps)
+    fl_lb = 2.0 * nb * mb * kk * nn
+    del Lb, Wb, Qb, Pb
+    torch.cuda.empty_cache()
 
     def line(key, name, ms, fl, dtype, shape, what):
         t = fl / (ms / 1e3) / 1e12
@@ -968,6 +981,9 @@ def gemm_bench(steps: int = 20):
                                  f"L^T [{m} x {kk}] (W - Q) [{kk} x {nn}] f64 (Q f32)", "2 M N K"),
         "ldlq_span_update_f32": line("ldlq_span_update", "gemm_tn_f32_kernel", ms_l, fl_l, "f32",
                                      f"L^T [{m} x {kk}] (W - Q) [{kk} x {nn}] f32", "2 M N K"),
+        "ldlq_span_update_batched": line("ldlq_span_update_batched_f64", "gemm_tn_f64_kernel (batched)", ms_lb, fl_lb,
+                                         "f64", f"{nb} members L^T [{mb} x {kk}] (W - Q) [{kk} x {nn}] f64 (Q f32)",
+                                         "2 batch M N K"),
     }
 
 
