@@ -208,9 +208,19 @@ def pack_records(encoded: torch.Tensor, rate_axis: str, record_bits) -> torch.Te
 
     from qsrt_amd.qsrt import pack_trellis_edges
 
-    axis = 0 if rate_axis == "k" else 1
-    pieces = [pack_trellis_edges(encoded.narrow(axis, 8 * r, 8).reshape(-1, 256), bits).reshape(-1)
-              for r, bits in enumerate(record_bits)]
+    tk, tn = encoded.shape[:2]
+    n_rec = len(record_bits)
+    if rate_axis == "k":  # a record is 8 whole tile rows: the records are already contiguous
+        by_record = encoded.reshape(n_rec, 8 * tn, 256)
+    else:  # a record is 8 tile columns: gather each record's tiles, row-major within it, in one copy
+        by_record = encoded.reshape(tk, n_rec, 8, 256).transpose(0, 1).reshape(n_rec, 8 * tk, 256)
+    pieces, r = [], 0
+    while r < n_rec:  # a run of consecutive records at one rate packs in one call (tiles pack independently)
+        e = r + 1
+        while e < n_rec and record_bits[e] == record_bits[r]:
+            e += 1
+        pieces.append(pack_trellis_edges(by_record[r:e].reshape(-1, 256), record_bits[r]).reshape(-1))
+        r = e
     return torch.cat(pieces)
 
 
