@@ -519,6 +519,7 @@ void decode_block_wave_kernel(const Job* __restrict__ jobs, int n_jobs, int64_t 
             constexpr int kChunks = kRowBytes / 16;
             constexpr int kTilesPerRound = kRowBytes / (16 * static_cast<int>(sizeof(OutT)));
             constexpr int kRounds = 8 / kTilesPerRound;
+            static_assert(kTilesPerRound % 2 == 0, "a tile-column pair stays within one staging round");
             char* out_row0 = cur.out + (16 * r) * cur.ld * sizeof(OutT);
 #pragma unroll
             for (int rd = 0; rd < kRounds; ++rd) {
