@@ -619,11 +619,16 @@ namespace {
 
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBK64 = 16;
+constexpr int kBM64 = 64;   // float64 tile: 64 rows of C x kBN columns, four waves of 32 x 64
+constexpr int kBK64 = 8;    // k-rows per LDS chunk (28 KB double-buffered: four workgroups per CU)
 constexpr int kPad64 = 16;  // row pad (doubles): the four k-rows of a fragment read start 32 banks apart
+constexpr int kMI64 = kBM64 / 32;                  // 16-row MFMA tiles per wave
+constexpr int kNA64 = kBK64 * kBM64 / 2 / kThreads;  // double2 of A per thread per chunk
+constexpr int kNB64 = kBK64 * kBN / 2 / kThreads;    // double2 of B per thread per chunk
+static_assert(kNA64 >= 1 && kNB64 >= 1 && kBK64 % 4 == 0, "float64 chunk shape");
 
 struct F64Chunk {
-    double2 a[4], b[4];
+    double2 a[kNA64], b[kNB64];
 };
 
 __device__ __forceinline__ double2 ld2_masked(const double* p, int64_t row, int64_t col, int64_t rows, int64_t cols,
@@ -649,10 +654,15 @@ __device__ __forceinline__ void load_f64(F64Chunk& ch, const double* A, const do
                                          int64_t m0, int64_t n0, int64_t M, int64_t N, int64_t K, int64_t lda,
                                          int64_t ldb, int64_t ldb2, int t) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int f = t + kThreads * i;  // 1024 double2 per operand chunk: 16 rows x 64 double2
-        const int r = f >> 6, q = f & 63;
+    for (int i = 0; i < kNA64; ++i) {  // kBK64 rows x kBM64 / 2 double2 of A
+        const int f = t + kThreads * i;
+        const int r = f / (kBM64 / 2), q = f % (kBM64 / 2);
         ch.a[i] = ld2_masked(A, k0 + r, m0 + 2 * q, K, M, lda);
+    }
+#pragma unroll
+    for (int i = 0; i < kNB64; ++i) {  // kBK64 rows x kBN / 2 double2 of B - B2
+        const int f = t + kThreads * i;
+        const int r = f / (kBN / 2), q = f % (kBN / 2);
         double2 b = ld2_masked(B, k0 + r, n0 + 2 * q, K, N, ldb);
         if (B2) {
             const double2 s = ld2_masked_f32(B2, k0 + r, n0 + 2 * q, K, N, ldb2);
@@ -663,28 +673,32 @@ __device__ __forceinline__ void load_f64(F64Chunk& ch, const double* A, const do
     }
 }
 
-__device__ __forceinline__ void store_f64(const F64Chunk& ch, double (*As)[kBM + kPad64], double (*Bs)[kBN + kPad64],
+__device__ __forceinline__ void store_f64(const F64Chunk& ch, double (*As)[kBM64 + kPad64], double (*Bs)[kBN + kPad64],
                                           int t) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < kNA64; ++i) {
         const int f = t + kThreads * i;
-        const int r = f >> 6, q = f & 63;
-        *reinterpret_cast<double2*>(&As[r][2 * q]) = ch.a[i];
-        *reinterpret_cast<double2*>(&Bs[r][2 * q]) = ch.b[i];
+        *reinterpret_cast<double2*>(&As[f / (kBM64 / 2)][2 * (f % (kBM64 / 2))]) = ch.a[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kNB64; ++i) {
+        const int f = t + kThreads * i;
+        *reinterpret_cast<double2*>(&Bs[f / (kBN / 2)][2 * (f % (kBN / 2))]) = ch.b[i];
     }
 }
 
-// Two waves per SIMD: 128 accumulator registers plus the operand chunk fit in 256.
+// Four workgroups per CU (four waves per SIMD): 64 accumulator registers per lane, 28 KB of LDS per workgroup,
+// so one workgroup's loads and stores of its C tile overlap the others' matrix-core work.
 // Batch members are consecutive runs of tiles_m * tiles_n workgroups (member-major, so a member's operands stay
 // in L2 while its tiles run); member b reads A + b * sa, B + b * sb, B2 + b * sb2 and updates C + b * sc.
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void gemm_tn_f64_kernel(double* __restrict__ C, const double* __restrict__ A,
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void gemm_tn_f64_kernel(double* __restrict__ C, const double* __restrict__ A,
                                                                const double* __restrict__ B,
                                                                const float* __restrict__ B2, int64_t M, int64_t N,
                                                                int64_t K, int64_t lda, int64_t ldb, int64_t ldb2,
                                                                int64_t ldc, double alpha, int64_t tiles_n,
                                                                int64_t tiles_per_member, int64_t sc, int64_t sa,
                                                                int64_t sb, int64_t sb2) {
-    __shared__ __attribute__((aligned(16))) double As[2][kBK64][kBM + kPad64];
+    __shared__ __attribute__((aligned(16))) double As[2][kBK64][kBM64 + kPad64];
     __shared__ __attribute__((aligned(16))) double Bs[2][kBK64][kBN + kPad64];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int c = lane & 15, g = lane >> 4;
@@ -693,18 +707,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     A += member * sa;
     B += member * sb;
     if (B2) B2 += member * sb2;
-    const int64_t m0 = (tile / tiles_n) * kBM, n0 = (tile % tiles_n) * kBN;
-    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int64_t m0 = (tile / tiles_n) * kBM64, n0 = (tile % tiles_n) * kBN;
+    const int wm = (wave >> 1) * (kBM64 / 2), wn = (wave & 1) * 64;
 
     const bool seed = alpha == 1.0;  // accumulators start from C (plain store at the end)
-    f64x4 acc[4][4];
+    f64x4 acc[kMI64][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kMI64; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f64x4{0.0, 0.0, 0.0, 0.0};
     if (seed) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < kMI64; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t row = m0 + wm + 16 * i + g + 4 * r;
@@ -726,13 +740,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         if (kc + 1 < chunks) load_f64(ch, A, B, B2, (kc + 1) * kBK64, m0, n0, M, N, K, lda, ldb, ldb2, t);
 #pragma unroll
         for (int kk = 0; kk < kBK64 / 4; ++kk) {
-            double a[4], b[4];
+            double a[kMI64], b[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) a[i] = As[cur][4 * kk + g][wm + 16 * i + c];
+            for (int i = 0; i < kMI64; ++i) a[i] = As[cur][4 * kk + g][wm + 16 * i + c];
 #pragma unroll
             for (int j = 0; j < 4; ++j) b[j] = Bs[cur][4 * kk + g][wn + 16 * j + c];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < kMI64; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i], b[j], acc[i][j], 0, 0, 0);
@@ -741,7 +755,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         __syncthreads();
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kMI64; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int64_t row = m0 + wm + 16 * i + g + 4 * r;
@@ -781,7 +795,7 @@ int qsrt_gemm_tn_f64_batched(double* C, const double* A, const double* B, const 
         return qsrt::fail(qsrt::kBadArgument, "gemm f64: member strides must be non-negative and even");
     if (batch > 1 && stride_c < (M - 1) * ldc + N)
         return qsrt::fail(qsrt::kBadArgument, "gemm f64: members of C overlap (stride_c < (M - 1) * ldc + N)");
-    const int64_t tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
+    const int64_t tiles_m = (M + kBM64 - 1) / kBM64, tiles_n = (N + kBN - 1) / kBN;
     if (tiles_m * tiles_n * batch > 0x7fffffff) return qsrt::fail(qsrt::kBadArgument, "gemm f64: too many tiles");
     hipLaunchKernelGGL(gemm_tn_f64_kernel, dim3(static_cast<unsigned>(tiles_m * tiles_n * batch)), dim3(kThreads), 0,
                        static_cast<hipStream_t>(stream_handle), C, A, B, B2, M, N, K, lda, ldb, ldb2, ldc, alpha,
