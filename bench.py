@@ -66,7 +66,7 @@ DECODE_TRAFFIC_OVER_ALGORITHMIC = 1.032
 # profiles/hadamard_kernel_expert_matrix.md): HBM bytes per launch (the Hessian capture: its main kernel and
 # the fixup kernel of its K-split tiles together).
 GEMM_HBM_BYTES = {"hessian_capture": 2.435e9, "ldlq_span_update": 1.485e8, "ldlq_span_update_f64": 2.950e8,
-                  "ldlq_span_update_batched_f64": 6.16e9}
+                  "ldlq_span_update_batched_f64": 6.09e9}
 HADAMARD_HBM_BYTES = {"left": 1.1782e8, "right": 1.1765e8}
 # Same counters for the BaKron top band's left + right launches (profiles/bakron_band_kernels_config4_gate.md):
 # mostly the right product's re-reads of the input factor.
