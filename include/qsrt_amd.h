@@ -309,6 +309,21 @@ int qsrt_chol_diag_block_f64(double *A, int64_t n, int64_t batch, int64_t batch_
                              double *inv, int32_t *info, void *stream);
 
 /*
+ * Unit block-lower factor of `batch` lower Cholesky factors, in place:
+ * C[b] = C + b * batch_stride (n x n, element (i, c) at i * row_stride +
+ * c * col_stride, one of the two strides 1; lower triangle holding the
+ * factor, zeros above).  With 16 x 16 column blocks j, rows i >= 16 j + 16
+ * become C[i, 16j:16j+16] inv[b][j], the diagonal blocks become the
+ * identity and the zeros above them are kept.  inv is [batch][n / 16][16][16]
+ * row-major, the inverses of the diagonal blocks.  n is a multiple of 16,
+ * the leading dimension at least n, batch <= 65535; row-major matrices need
+ * 16-byte aligned rows.  Replaces the column-block products and identity
+ * blocks of block_ldl (qsrt/exl3_encoder_backend.py:375-390).
+ */
+int qsrt_block_unit_lower_f64(double *C, const double *inv, int64_t batch, int64_t n, int64_t row_stride,
+                              int64_t col_stride, int64_t batch_stride, void *stream);
+
+/*
  * One band propagation of the recursive BaKron two-sided rounding, FP32,
  * 16 x 16 blocks.  workspace (T), quantized (Q) and intermediate (I) are
  * [batch, n_out, n_in] row-major; output_factor and input_factor are

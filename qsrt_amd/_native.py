@@ -79,6 +79,9 @@ SIGNATURES: dict[str, tuple] = {
     "qsrt_chol_diag_block_f64": (
         _c_int, [_c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_void_p, _c_void_p, _c_void_p],
     ),
+    "qsrt_block_unit_lower_f64": (
+        _c_int, [_c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p],
+    ),
     "qsrt_bakron_band_update_f32": (
         _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                  _c_i64, _c_i64, _c_i64, _c_void_p],

@@ -178,7 +178,93 @@ __global__ __launch_bounds__(kThreadsChol) void chol_diag_block_f64_kernel(doubl
 
 }  // namespace
 
+// Unit block-lower factor from a lower Cholesky factor, in place: row i of column block j (i past the block's
+// diagonal) becomes C[i, 16 j : 16 j + 16] inv_j, the diagonal 16 x 16 blocks become the identity, and the zero
+// blocks above the diagonal are not touched.  One workgroup per (row chunk, column block, matrix); inv_j is
+// staged in LDS and each thread owns one row: sixteen doubles read, sixteen 16-term products, sixteen written.
+// Element (i, c) sits at i * ld + c (row-major, 16-byte loads along the row) or at c * ld + i (column-major, the
+// layout torch's batched Cholesky returns: a wave's 64 rows are then 512 contiguous bytes per column).
+constexpr int kUnitRows = 256;
+
+template <bool kRowMajor>
+__global__ __launch_bounds__(kUnitRows) void block_unit_lower_f64_kernel(double* __restrict__ C,
+                                                                         const double* __restrict__ inv, int64_t n,
+                                                                         int64_t ld, int64_t batch_stride) {
+    const int64_t j = blockIdx.y, mat = blockIdx.z;
+    const int64_t col0 = 16 * j;
+    const int64_t row0 = col0 + static_cast<int64_t>(blockIdx.x) * kUnitRows;
+    if (row0 >= n) return;  // the whole workgroup is past the last row
+    __shared__ double iv[16][17];
+    const double* ij = inv + (mat * (n / 16) + j) * 256;
+    for (int e = threadIdx.x; e < 256; e += kUnitRows) iv[e >> 4][e & 15] = ij[e];
+    __syncthreads();
+    const int64_t row = row0 + threadIdx.x;
+    if (row >= n) return;
+    double* base = C + mat * batch_stride;
+    const int64_t rs = kRowMajor ? ld : 1, cs = kRowMajor ? 1 : ld;
+    double* r = base + row * rs + col0 * cs;
+    if (row < col0 + 16) {  // the diagonal block
+#pragma unroll
+        for (int l = 0; l < 16; ++l) r[l * cs] = (row - col0 == l) ? 1.0 : 0.0;
+        return;
+    }
+    double x[16];
+    if constexpr (kRowMajor) {
+#pragma unroll
+        for (int k = 0; k < 16; k += 2) {
+            const double2 v = *reinterpret_cast<const double2*>(r + k);
+            x[k] = v.x;
+            x[k + 1] = v.y;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) x[k] = r[k * cs];
+    }
+#pragma unroll
+    for (int l = 0; l < 16; l += 2) {
+        double a0 = 0.0, a1 = 0.0;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            a0 = __builtin_fma(x[k], iv[k][l], a0);
+            a1 = __builtin_fma(x[k], iv[k][l + 1], a1);
+        }
+        if constexpr (kRowMajor) {
+            *reinterpret_cast<double2*>(r + l) = make_double2(a0, a1);
+        } else {
+            r[l * cs] = a0;
+            r[(l + 1) * cs] = a1;
+        }
+    }
+}
+
 extern "C" {
+
+int qsrt_block_unit_lower_f64(double* C, const double* inv, int64_t batch, int64_t n, int64_t row_stride,
+                              int64_t col_stride, int64_t batch_stride, void* stream_handle) {
+    hipStream_t stream = static_cast<hipStream_t>(stream_handle);
+    if (!C || !inv) return qsrt::fail(qsrt::kBadArgument, "null pointer argument");
+    if (n <= 0 || batch <= 0) return qsrt::fail(qsrt::kBadArgument, "n and batch must be positive");
+    if (n % 16) return qsrt::fail(qsrt::kBadArgument, "n must be a multiple of 16");
+    const bool row_major = col_stride == 1;
+    if (!row_major && row_stride != 1)
+        return qsrt::fail(qsrt::kBadArgument, "one of row_stride and col_stride must be 1");
+    const int64_t ld = row_major ? row_stride : col_stride;
+    if (ld < n) return qsrt::fail(qsrt::kBadArgument, "the leading dimension must be at least n");
+    if (row_major && (ld % 2 || reinterpret_cast<uintptr_t>(C) % 16 || (batch > 1 && batch_stride % 2)))
+        return qsrt::fail(qsrt::kBadArgument, "row-major matrices need 16-byte aligned rows");
+    if (batch > 1 && batch_stride < (n - 1) * ld + n)
+        return qsrt::fail(qsrt::kBadArgument, "the batch stride must keep the matrices apart");
+    if (batch > 65535 || n / 16 > 65535) return qsrt::fail(qsrt::kBadArgument, "batch or n too large for one launch");
+    const dim3 grid(static_cast<unsigned>((n + kUnitRows - 1) / kUnitRows), static_cast<unsigned>(n / 16),
+                    static_cast<unsigned>(batch));
+    const int64_t bs = batch > 1 ? batch_stride : 0;
+    if (row_major)
+        hipLaunchKernelGGL(block_unit_lower_f64_kernel<true>, grid, dim3(kUnitRows), 0, stream, C, inv, n, ld, bs);
+    else
+        hipLaunchKernelGGL(block_unit_lower_f64_kernel<false>, grid, dim3(kUnitRows), 0, stream, C, inv, n, ld, bs);
+    QSRT_HIP_TRY(hipGetLastError());
+    return qsrt::kOk;
+}
 
 int qsrt_chol_diag_block_f64(double* A, int64_t n, int64_t batch, int64_t batch_stride, int64_t j0, int nb,
                              double* inv, int32_t* info, void* stream_handle) {

@@ -146,3 +146,58 @@ def test_bad_arguments_are_rejected():
         with pytest.raises(ValueError):
             _native.check(lib.qsrt_chol_diag_block_f64(A.data_ptr(), n, batch, stride, j0, nb, inv.data_ptr(),
                                                         info.data_ptr(), s), "chol")
+
+
+def _block_diag_of(C: torch.Tensor, b: int = 16) -> torch.Tensor:
+    n = C.shape[-1]
+    m = n // b
+    return torch.diagonal(C.view(-1, m, b, m, b), dim1=1, dim2=3).permute(0, 3, 1, 2)
+
+
+@pytest.mark.parametrize("n,batch,layout", [(16, 1, "row"), (1024, 1, "row"), (1024, 3, "row"), (784, 2, "col"),
+                                            (16, 2, "col")])
+def test_block_unit_lower_matches_the_column_block_products(n, batch, layout):
+    """``qsrt_block_unit_lower_f64`` on row-major factors (the blocked
+    Cholesky's) and column-major ones (torch's batched Cholesky's): equal to
+    the torch column-block products within float64 rounding, exact identity
+    diagonal blocks, the zeros above left alone, and ``L D L^T`` gives the
+    matrix back (``D`` the blocks ``C_jj C_jj^T``)."""
+
+    from qsrt_amd.cholesky import block_unit_lower_f64_
+
+    print(f"[block_unit_lower] n {n} batch {batch} {layout}", file=sys.stderr, flush=True)
+    A = torch.stack([_spd(n, 60 + b) for b in range(batch)])
+    C = torch.linalg.cholesky(A)
+    if layout == "row":
+        C = C.contiguous()
+    else:
+        C = C.mT.contiguous().mT
+    assert (C.stride(2) == 1) == (layout == "row")
+    inv = torch.linalg.inv(_block_diag_of(C))
+    D = _block_diag_of(C) @ _block_diag_of(C).mT
+    ref = block_unit_lower_f64_(C.cpu().clone(), inv.cpu())
+    out = block_unit_lower_f64_(C, inv)
+    torch.cuda.synchronize()
+    assert out.data_ptr() == C.data_ptr()
+    assert (out.cpu() - ref).abs().max().item() <= 1e-13 * ref.abs().max().item()
+    m = n // 16
+    blocks = out.view(batch, m, 16, m, 16).permute(0, 1, 3, 2, 4)
+    idx = torch.arange(m, device=DEV)
+    assert torch.equal(blocks[:, idx, idx], torch.eye(16, dtype=torch.float64, device=DEV).expand(batch, m, 16, 16))
+    assert torch.equal(out, out.tril())
+    Dfull = torch.block_diag(*D.reshape(-1, 16, 16)).view(batch, m * 16, batch, m * 16)
+    Dfull = torch.stack([Dfull[b, :, b] for b in range(batch)])
+    assert (out @ Dfull @ out.mT - A).abs().max().item() <= 1e-12 * A.abs().max().item()
+
+
+def test_block_unit_lower_rejects_bad_arguments():
+    lib = _native.lib()
+    C = torch.zeros(2, 32, 32, dtype=torch.float64, device=DEV)
+    inv = torch.zeros(2, 2, 16, 16, dtype=torch.float64, device=DEV)
+    s = _native.stream_handle(DEV)
+    # n not a multiple of 16, no unit stride, leading dimension < n, overlapping members, odd row stride
+    for n, rs, cs, bs, batch in ((24, 32, 1, 1024, 2), (32, 32, 2, 1024, 2), (32, 16, 1, 1024, 2),
+                                 (32, 32, 1, 512, 2), (32, 33, 1, 1056, 1), (0, 32, 1, 1024, 2)):
+        with pytest.raises(ValueError):
+            _native.check(lib.qsrt_block_unit_lower_f64(C.data_ptr(), inv.data_ptr(), batch, n, rs, cs, bs, s),
+                          "unit")
