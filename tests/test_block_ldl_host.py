@@ -47,3 +47,27 @@ def test_block_unit_lower_checks_its_arguments():
     with pytest.raises(ValueError, match="inv_blocks"):
         block_unit_lower_f64_(torch.zeros(2, 32, 32, dtype=torch.float64), torch.zeros(2, 1, 16, 16,
                                                                                         dtype=torch.float64))
+
+
+@pytest.mark.parametrize("n,N,block", [(64, 24, 16), (272, 40, 128), (300, 7, 1024)])
+def test_symmetric_trace_equals_the_full_trace(n, N, block):
+    """``symmetric_trace_parts`` (the proxy errors' half-product trace)
+    against ``trace(A^T H A)`` in float64 and against the reference-shaped
+    ``block_trace``: equal to FP32 rounding for a symmetric ``H``, blocks
+    that do not divide ``n`` included; it reads ``H``'s lower block triangle
+    only (the blocks above the diagonal blocks may hold anything)."""
+
+    from qsrt_amd.exl3_encoder_backend import block_trace, symmetric_trace_parts
+
+    g = torch.Generator().manual_seed(n + N)
+    H = _spd(n, n + 1).float()
+    A = torch.randn(n, N, generator=g)
+    exact = float(torch.trace(A.double().T @ H.double() @ A.double()))
+    got = float(symmetric_trace_parts(A, H, block).double().sum())
+    assert abs(got - exact) <= 1e-5 * exact
+    assert abs(got - block_trace(A, H)) <= 1e-5 * exact
+    rows = torch.arange(n) // block
+    upper_blocks = rows.unsqueeze(1) < rows.unsqueeze(0)
+    H2 = H.clone()
+    H2[upper_blocks] += 1.0
+    assert float(symmetric_trace_parts(A, H2, block).double().sum()) == got
