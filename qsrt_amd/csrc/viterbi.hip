@@ -15,7 +15,9 @@
 //   * 2^K states sharing one predecessor set are evaluated together, so
 //     every LDS cost read serves 2^K edges;
 //   * per state: d = label - x, c = fma(d, d, cost[pred]), value = min3
-//     chain, decision = lowest k with c == value (lowest-index ties);
+//     chain, decision = lowest k with c == value (lowest-index ties): wave
+//     ballots and scalar mask algebra at K1/K2, a compare-and-select scan in
+//     VGPRs at K3/K4;
 //   * K5 / K6 (32 / 64 predecessors per state) stream the predecessors
 //     through a running minimum instead of holding them in registers;
 //   * decisions are packed (K bits per state, 1..32 bits per thread) into
@@ -324,11 +326,17 @@ __device__ __forceinline__ void trellis_step(const Labels<K>& lab, const float* 
             for (int k = 1; k < G::P; ++k) m = fmin2(m, c[k]);
             best[e] = m;
             if constexpr (RECORD) {
-                if constexpr (K <= 3) {
+                if constexpr (K <= 2) {
                     word = push_argmin<K>(word, c, m);
                 } else {
-                    // 16 predecessors: the mask algebra would cost ~37 scalar
-                    // ops per state, so select the index in VGPRs instead.
+                    // K3 and K4: select the index in VGPRs (P - 1 compares and
+                    // selects, one shift-or).  The ballot form issues fewer
+                    // VALU ops (K3: 10 against 15 per state) but its scalar
+                    // mask algebra (K3: ~16 ops per state, K4: ~36), fed by
+                    // VALU compares and feeding VALU pushes, is the slower
+                    // chain: on 65,536 tiles K3 takes 186 ms with selects and
+                    // 211 ms with ballots, K4 190 against 219 (K2, 3 compares
+                    // per state, is faster with ballots: 187 against 190).
                     int arg = G::P - 1;
 #pragma unroll
                     for (int k = G::P - 2; k >= 0; --k) arg = (c[k] == m) ? k : arg;
