@@ -15,9 +15,9 @@
 //   * 2^K states sharing one predecessor set are evaluated together, so
 //     every LDS cost read serves 2^K edges;
 //   * per state: d = label - x, c = fma(d, d, cost[pred]), value = min3
-//     chain, decision = lowest k with c == value (lowest-index ties): wave
-//     ballots and scalar mask algebra at K1/K2, a compare-and-select scan in
-//     VGPRs at K3/K4;
+//     chain, decision = lowest k with c == value (lowest-index ties), read
+//     off a tournament over the minimum's own tree on the recorded steps
+//     (K2..K4; K1 uses wave ballots);
 //   * K5 / K6 (32 / 64 predecessors per state) stream the predecessors
 //     through a running minimum instead of holding them in registers;
 //   * decisions are packed (K bits per state, 1..32 bits per thread) into
@@ -163,16 +163,6 @@ __device__ __forceinline__ uint32_t push_bit(uint32_t word, uint64_t mask) {
     return out;
 }
 
-// word = (word << B) | value in one v_lshl_or_b32.  Opaque to the compiler
-// on purpose: a visible constant shift gets folded into the index selects,
-// which then materialise dozens of pre-shifted constants in VGPRs.
-template <int B>
-__device__ __forceinline__ uint32_t push_bits(uint32_t word, uint32_t value) {
-    uint32_t out;
-    asm("v_lshl_or_b32 %0, %1, %2, %3" : "=v"(out) : "v"(word), "i"(B), "v"(value));
-    return out;
-}
-
 // Pack the lowest-index argmin of c[0..P) (value m) into `word`, K bits, MSB
 // first.  The P-1 equality tests are wave ballots (SGPR lane masks); the
 // prefix masks ge[k] = "argmin >= k" and the bit masks are scalar-unit
@@ -193,6 +183,64 @@ __device__ __forceinline__ uint32_t push_argmin(uint32_t word, const float (&c)[
         word = push_bit(word, bit);
     }
     return word;
+}
+
+// Minimum of c[0..P) and its lowest index pushed into `word` (K bits, MSB
+// first) as a tournament whose levels are read off the minimum's own tree:
+// bit K-1 says whether the lower half's minimum misses the overall one, the
+// next bit the same of the first quarter of the chosen half, and so on down to
+// the chosen pair's first element.  The minimum is exact whatever the order,
+// so it equals the plain min3 chain; "equal to the minimum" at each level
+// keeps the lowest index, so the bits equal a lowest-index scan.  K3: 5
+// min/min3 + 3 compares + 4 selects + 3 pushes = 15 VALU per state (a scan
+// with P - 1 compares and selects takes 19); K4: 11 + 4 + 11 + 4 = 30 (39).
+template <int K>
+__device__ __forceinline__ float min_push_argmin(uint32_t& word, const float (&c)[1 << K]) {
+    if constexpr (K == 2) {
+        const float p0 = fmin2(c[0], c[1]);
+        const float m = fmin2(p0, fmin2(c[2], c[3]));
+        const bool b1 = p0 != m;
+        const float e = b1 ? c[2] : c[0];
+        const bool b0 = e != m;
+        word = push_bit(word, __builtin_amdgcn_ballot_w64(b1));
+        word = push_bit(word, __builtin_amdgcn_ballot_w64(b0));
+        return m;
+    } else if constexpr (K == 3) {
+        const float p0 = fmin2(c[0], c[1]), p2 = fmin2(c[4], c[5]);
+        const float h0 = fmin2(p0, fmin2(c[2], c[3])), h1 = fmin2(p2, fmin2(c[6], c[7]));
+        const float m = fmin2(h0, h1);
+        const bool b2 = h0 != m;
+        const float q = b2 ? p2 : p0;
+        const bool b1 = q != m;
+        const float e = b2 ? (b1 ? c[6] : c[4]) : (b1 ? c[2] : c[0]);
+        const bool b0 = e != m;
+        word = push_bit(word, __builtin_amdgcn_ballot_w64(b2));
+        word = push_bit(word, __builtin_amdgcn_ballot_w64(b1));
+        word = push_bit(word, __builtin_amdgcn_ballot_w64(b0));
+        return m;
+    } else {
+        static_assert(K == 4, "tournament argmin is written for K2..K4");
+        const float p0 = fmin2(c[0], c[1]), p2 = fmin2(c[4], c[5]), p4 = fmin2(c[8], c[9]),
+                    p6 = fmin2(c[12], c[13]);
+        const float q0 = fmin2(p0, fmin2(c[2], c[3])), q1 = fmin2(p2, fmin2(c[6], c[7]));
+        const float q2 = fmin2(p4, fmin2(c[10], c[11])), q3 = fmin2(p6, fmin2(c[14], c[15]));
+        const float h0 = fmin2(q0, q1), h1 = fmin2(q2, q3);
+        const float m = fmin2(h0, h1);
+        const bool b3 = h0 != m;
+        const float q = b3 ? q2 : q0;
+        const bool b2 = q != m;
+        const float p = b3 ? (b2 ? p6 : p4) : (b2 ? p2 : p0);
+        const bool b1 = p != m;
+        const float s0 = b1 ? c[2] : c[0], s1 = b1 ? c[6] : c[4], s2 = b1 ? c[10] : c[8], s3 = b1 ? c[14] : c[12];
+        const float t0 = b2 ? s1 : s0, t1 = b2 ? s3 : s2;
+        const float e = b3 ? t1 : t0;
+        const bool b0 = e != m;
+        word = push_bit(word, __builtin_amdgcn_ballot_w64(b3));
+        word = push_bit(word, __builtin_amdgcn_ballot_w64(b2));
+        word = push_bit(word, __builtin_amdgcn_ballot_w64(b1));
+        word = push_bit(word, __builtin_amdgcn_ballot_w64(b0));
+        return m;
+    }
 }
 
 // Predecessor cost of the first step of a pass: 0 for every predecessor, or,
@@ -321,27 +369,13 @@ __device__ __forceinline__ void trellis_step(const Labels<K>& lab, const float* 
                 const float d = lab.v[j][e][k] - x;
                 c[k] = __builtin_fmaf(d, d, p[k]);
             }
-            float m = c[0];
-#pragma unroll
-            for (int k = 1; k < G::P; ++k) m = fmin2(m, c[k]);
-            best[e] = m;
             if constexpr (RECORD) {
-                if constexpr (K <= 2) {
-                    word = push_argmin<K>(word, c, m);
-                } else {
-                    // K3 and K4: select the index in VGPRs (P - 1 compares and
-                    // selects, one shift-or).  The ballot form issues fewer
-                    // VALU ops (K3: 10 against 15 per state) but its scalar
-                    // mask algebra (K3: ~16 ops per state, K4: ~36), fed by
-                    // VALU compares and feeding VALU pushes, is the slower
-                    // chain: on 65,536 tiles K3 takes 186 ms with selects and
-                    // 211 ms with ballots, K4 190 against 219 (K2, 3 compares
-                    // per state, is faster with ballots: 187 against 190).
-                    int arg = G::P - 1;
+                best[e] = min_push_argmin<K>(word, c);
+            } else {
+                float m = c[0];
 #pragma unroll
-                    for (int k = G::P - 2; k >= 0; --k) arg = (c[k] == m) ? k : arg;
-                    word = push_bits<K>(word, static_cast<uint32_t>(arg));
-                }
+                for (int k = 1; k < G::P; ++k) m = fmin2(m, c[k]);
+                best[e] = m;
             }
             // One state at a time: four waves per SIMD already hide latency,
             // and overlapping states would push the labels out of VGPRs.
