@@ -191,9 +191,12 @@ __device__ __forceinline__ uint32_t push_argmin(uint32_t word, const float (&c)[
 // next bit the same of the first quarter of the chosen half, and so on down to
 // the chosen pair's first element.  The minimum is exact whatever the order,
 // so it equals the plain min3 chain; "equal to the minimum" at each level
-// keeps the lowest index, so the bits equal a lowest-index scan.  K3: 5
-// min/min3 + 3 compares + 4 selects + 3 pushes = 15 VALU per state (a scan
-// with P - 1 compares and selects takes 19); K4: 11 + 4 + 11 + 4 = 30 (39).
+// keeps the lowest index, so the bits equal a lowest-index scan.  At K3/K4
+// the root is a compare (right half strictly smaller) and a select, which
+// gives the top bit and the minimum in one compare.  K3: 4 min/min3 + 3
+// compares + 5 selects + 3 pushes = 15 VALU per state (a scan with P - 1
+// compares and selects takes 19); K4: 10 + 4 + 12 + 4 = 30 (39).  On gfx950 a
+// select issues in half the cycles of a min, a compare or an FMA.
 template <int K>
 __device__ __forceinline__ float min_push_argmin(uint32_t& word, const float (&c)[1 << K]) {
     if constexpr (K == 2) {
@@ -208,8 +211,8 @@ __device__ __forceinline__ float min_push_argmin(uint32_t& word, const float (&c
     } else if constexpr (K == 3) {
         const float p0 = fmin2(c[0], c[1]), p2 = fmin2(c[4], c[5]);
         const float h0 = fmin2(p0, fmin2(c[2], c[3])), h1 = fmin2(p2, fmin2(c[6], c[7]));
-        const float m = fmin2(h0, h1);
-        const bool b2 = h0 != m;
+        const bool b2 = h1 < h0;  // the root as compare-and-select: the compare is needed anyway
+        const float m = b2 ? h1 : h0;
         const float q = b2 ? p2 : p0;
         const bool b1 = q != m;
         const float e = b2 ? (b1 ? c[6] : c[4]) : (b1 ? c[2] : c[0]);
@@ -225,8 +228,8 @@ __device__ __forceinline__ float min_push_argmin(uint32_t& word, const float (&c
         const float q0 = fmin2(p0, fmin2(c[2], c[3])), q1 = fmin2(p2, fmin2(c[6], c[7]));
         const float q2 = fmin2(p4, fmin2(c[10], c[11])), q3 = fmin2(p6, fmin2(c[14], c[15]));
         const float h0 = fmin2(q0, q1), h1 = fmin2(q2, q3);
-        const float m = fmin2(h0, h1);
-        const bool b3 = h0 != m;
+        const bool b3 = h1 < h0;
+        const float m = b3 ? h1 : h0;
         const float q = b3 ? q2 : q0;
         const bool b2 = q != m;
         const float p = b3 ? (b2 ? p6 : p4) : (b2 ? p2 : p0);
@@ -377,9 +380,6 @@ __device__ __forceinline__ void trellis_step(const Labels<K>& lab, const float* 
                 for (int k = 1; k < G::P; ++k) m = fmin2(m, c[k]);
                 best[e] = m;
             }
-            // One state at a time: four waves per SIMD already hide latency,
-            // and overlapping states would push the labels out of VGPRs.
-            __builtin_amdgcn_sched_barrier(0);
         }
         float* dst = next + G::first_state(t, j);
 #pragma unroll
