@@ -54,8 +54,6 @@ FP32_PEAK_TFLOPS = 157.3
 FP32_UNPACKED_PEAK_TFLOPS = 78.6  # 256 CUs x 64 FP32 FMA lanes x 2 flops x 2.4 GHz, no packed FP32
 HBM_PEAK_GBPS = 8000.0
 MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "f32": 157.3, "f64": 78.6}
-# VALU issue-slot occupancy of viterbi_tiles_kernel by PMC (profiles/viterbi_tiles_kernel_microbench.md)
-VITERBI_VALU_ISSUE_FRAC_PMC = {"K2": 1.06, "K3": 0.94}
 # HBM bytes per tile of the Viterbi kernel by rate (FETCH_SIZE x 2.00 + WRITE_SIZE x 1.00 per dispatch, calibrated
 # on a 4 GiB device copy; K3/K4 over every dispatch of a 20-expert layer step, K2 from the microbench;
 # profiles/layer_encode_config5.md): mostly the traceback decision stream.
