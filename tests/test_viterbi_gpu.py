@@ -52,6 +52,30 @@ def test_gpu_matches_oracle_bit_exact(bits, context, lag):
     assert np.array_equal(recon, o_recon)
 
 
+@pytest.mark.parametrize("bits", (2, 3, 4))
+def test_gpu_tie_heavy_tiles_match_oracle(bits):
+    """Tiles drawn from a handful of the codebook's own values (and their
+    negatives, and zero): many edges cost exactly the same, so the
+    lowest-index rule decides most decisions.  The tournament argmin of the
+    recorded steps (pair minima, the root as compare-and-select, one
+    compare per level against the minimum) must pick the same predecessor
+    as the oracle's scan on every tie."""
+
+    _say(f"[viterbi] K{bits}: 32 tie-heavy tiles")
+    values = np.unique(np.abs(otables.t12_values(bits).astype(np.float32)))
+    rng = np.random.default_rng(300 + bits)
+    pool = np.concatenate([values[rng.choice(values.size, 3, replace=False)], [0.0]]).astype(np.float32)
+    pool = np.concatenate([pool, -pool])
+    tiles = rng.choice(pool, size=(32, 256)).astype(np.float32)
+    tiles[5] = pool[0]
+    tiles[9] = 0.0
+    recon, states = _gpu(tiles, bits, 128, 0 if bits == 2 else 1)
+    o_recon, o_states = ov.encode(tiles, otables.t12_values(bits), K=bits, boundary_lag=0 if bits == 2 else 1)
+    mismatch = (states != o_states).any(axis=1)
+    assert not mismatch.any(), f"{int(mismatch.sum())} tiles differ, first {int(np.flatnonzero(mismatch)[0])}"
+    assert np.array_equal(recon, o_recon)
+
+
 @pytest.mark.parametrize("bits", (1, 2, 3, 4, 5, 6))
 def test_gpu_many_tiles_persistent_loop(bits):
     """More tiles than workgroups: every workgroup walks several tiles."""
