@@ -202,7 +202,53 @@ def test_factored_hessian_stays_on_the_device():
     assert shared["L"] is L_obj and proxy2 == pytest.approx(proxy, rel=1e-6)
 
 
-def test_quantize_uniform_batch_shared_hessian_matches_single():
+@pytest.mark.parametrize("shared_h", [True, False])
+def test_quantize_uniform_batch_equals_single_encodes(shared_h):
+    """The same-K batch API against one ``quantize_qsrt`` per tensor on
+    fresh Hessian dicts: equal packed trellis, sign/scale vectors, global
+    scale and output-scale decision, the proxy error to FP32 rounding, and
+    the caller's weight left regularised the same way.  Shared Hessian: the
+    members concatenated along N under one factor; distinct Hessians:
+    stacked, one factor each, with one member whose Hessian is empty (the
+    fallback encode)."""
+
+    _say(f"[backend] quantize_uniform_batch vs single encodes, shared H {shared_h}")
+    k, n, members = 256, 256, 3
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(77)
+    Ws = [torch.from_numpy((rng.standard_normal((k, n)) * 0.02).astype(np.float32)).to(dev) for _ in range(members)]
+    Hs = []
+    for i in range(1 if shared_h else members):
+        x = _ar1(1024, k, 0.8, 90 + i)
+        Hs.append(torch.from_numpy(x.T @ x).float())
+
+    def h_data(i):
+        d = make_shared_h(k, dev, Hs[0 if shared_h else i])
+        d["count"] = 0 if (not shared_h and i == members - 1) else 1024
+        return d
+
+    if shared_h:
+        one = h_data(0)
+        batch_h = [one] * members
+    else:
+        batch_h = [h_data(i) for i in range(members)]
+    qas_b = [_qa(3, sv_seed=200 + i) for i in range(members)]
+    batch_w = [w.clone() for w in Ws]
+    out = be.quantize_uniform_batch(list(batch_w), batch_h, qas_b)
+    for i in range(members):
+        qa_s = _qa(3, sv_seed=200 + i)
+        w_s = Ws[i].clone()
+        _, proxy_s, tensors_s = be.quantize_qsrt(w_s, h_data(i), qa_s, False)
+        proxy_b, tensors_b = out[i]
+        assert torch.equal(tensors_b["trellis"], tensors_s["trellis"]), f"member {i}"
+        assert torch.equal(tensors_b["suh"], tensors_s["suh"]) and torch.equal(tensors_b["svh"], tensors_s["svh"])
+        for key in ("g_scale", "apply_out_scales", "q_fallback"):
+            assert qas_b[i][key] == qa_s[key], (i, key)
+        assert proxy_b == pytest.approx(proxy_s, rel=1e-6)
+        assert torch.equal(batch_w[i], w_s)
+
+
+def test_quantize_uniform_batch_shared_hessian_payloads_close():
     _say("[backend] quantize_uniform_batch shared H")
     k, n = 256, 256
     x = _ar1(2048, k, 0.85, 40)
