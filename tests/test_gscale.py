@@ -107,3 +107,16 @@ def test_sample_scale_tiles_is_the_wrapped_diagonal_plus_extreme_rms():
     hi = list(range(kt * nt - 1, kt * nt - 1 - extremes, -1))
     lo = list(range(extremes))
     assert ids == diagonal + hi + lo
+
+
+def test_sample_scale_tiles_elements_in_tensor_core_order():
+    # element (r, c) of every tile holds its row-major index r * 16 + c, so each sampled tile must read back as
+    # the tensor-core permutation itself; a ragged shape (3 x 7 tiles) exercises the wrap in both directions
+    kt, nt = 3, 7
+    idx = torch.arange(256, dtype=torch.float32).view(16, 16)
+    w = idx.repeat(kt, nt).contiguous()
+    tiles = be.sample_scale_tiles(w, width=2)
+    perm = be.tensor_core_perm("cpu").float()
+    assert tiles.dtype == torch.float32 and tiles.shape[1] == 256
+    assert torch.equal(tiles, perm.expand_as(tiles))
+    assert sorted(set(perm.long().tolist())) == list(range(256))

@@ -98,3 +98,56 @@ def test_objectives_and_config_keys():
     assert (cfg.sweeps, cfg.dither_scales, cfg.num_dither_patterns, cfg.score_dtype, cfg.alternate_sweep_order,
             cfg.seed, cfg.max_quantizer_batch) == (3, (0.5,), 4, torch.float64, False, 9, 64)
     assert hr.config_from_quant_args({}) == hr.H2ViterbiRefineConfig()
+
+
+def test_uniform_candidate_entry_rate_and_refusals(monkeypatch):
+    """``refine_uniform_h2_candidate`` (reference ``qsrt/exl3_encoder_backend.py:840-895``): no sweeps returns
+    the candidate with the disabled receipt; a uniform rate map refines at that rate through a plain-``K``
+    quantizer; every contract one callback cannot honour is refused before any work."""
+
+    from qsrt_amd import exl3_encoder_backend as be
+
+    calls = []
+
+    class _Result:
+        weight_q, encoded = "Q1", "S1"
+
+        @staticmethod
+        def stats_dict():
+            return {"sweeps": ["s"]}
+
+    def fake_refine(weight, hessian, weight_q, encoded, quantizer, config, guidance=None):
+        quantizer("tiles")
+        calls.append((config, guidance))
+        return _Result
+
+    def fake_quantize(tiles, args):
+        calls.append(dict(args))
+
+    monkeypatch.setattr(be.h2_viterbi_refine, "refine_h2_viterbi_paths", fake_refine)
+    monkeypatch.setattr(be, "quantize_tiles_multigpu", fake_quantize)
+    W, H = torch.zeros(32, 48), torch.eye(32)
+    base = {"K": 2, "devices": [0]}
+    assert be.refine_uniform_h2_candidate(W, H, "Q0", "S0", dict(base)) == ("Q0", "S0", {"enabled": False,
+                                                                                    "sweeps": []})
+    assert calls == []
+    mixed = dict(base, h2_viterbi_refine_sweeps=2, h2_viterbi_refine_patterns=3, mixed_rate_axis="n",
+                 mixed_tile_bits=(3, 3, 3))
+    q, s, receipt = be.refine_uniform_h2_candidate(W, H, "Q0", "S0", mixed, guidance="g")
+    assert (q, s, receipt) == ("Q1", "S1", {"enabled": True, "rate_bits": 3, "sweeps": ["s"]})
+    args, (config, guidance) = calls
+    assert args["K"] == 3 and "mixed_rate_axis" not in args and "mixed_tile_bits" not in args
+    assert (config.sweeps, config.num_dither_patterns, guidance) == (2, 3, "g")
+    assert mixed["K"] == 2 and mixed["mixed_tile_bits"] == (3, 3, 3)  # the caller's arguments are untouched
+    on = dict(base, h2_viterbi_refine_sweeps=1)
+    refusals = [
+        (dict(on, periodic_rate_schedules=[(2, 3)]), "one fixed tile rate"),
+        (dict(on, devices=[0, 1]), "one quantizer device"),
+        (dict(on, mixed_rate_axis="k", mixed_tile_bits=(2, 3)), "uniform rate map"),
+        (dict(on, mixed_tile_codebook_ids=[0]), "tile-local codebook selectors"),
+    ]
+    calls.clear()
+    for args, message in refusals:
+        with pytest.raises(ValueError, match=message):
+            be.refine_uniform_h2_candidate(W, H, "Q0", "S0", args)
+    assert calls == []
