@@ -638,7 +638,7 @@ def _sign_draw(n: int, seed: int):
     return (torch.randn(n, generator=g).sign() + 1e-5).sign().double().numpy()
 
 
-def layer_cpu_sample(first: dict, source: dict, blocks: int = 96) -> dict:
+def layer_cpu_sample(first: dict, source: dict, blocks: int = 160) -> dict:
     """The CPU oracle on the layer's first expert, w1, over the bottom
     ``blocks`` 16-row blocks -- the first steps of the backward recursion,
     which depend on nothing above them.  Two comparisons with the GPU's
